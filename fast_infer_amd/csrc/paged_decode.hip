@@ -1,0 +1,435 @@
+// Paged-attention decode for gfx950: one query token per sequence attends to its
+// context stored in a paged KV pool [num_blocks, block_size, num_kv_heads, 128].
+//
+// Replaces _paged_attention_kernel (kernels/attention.py:116-188).  Same math —
+// scores q.k * sm_scale over the first ctx tokens, softmax, weighted sum of V — but
+// organised for an HBM-bound MI355X kernel:
+//   * one workgroup serves all query heads of a GQA group, so each K/V row is read
+//     from HBM once (the reference reads it once per query head, :137-139);
+//   * the context is split into partitions (flash-decoding); each workgroup turns one
+//     partition into an unnormalised partial (m, l, o) and a second small kernel
+//     merges the partials; a single-partition call writes the output directly;
+//   * QK^T and PV run on MFMA (v_mfma_f32_16x16x32_f16) with the GQA heads as the
+//     16-wide N dimension: S^T = K * Q^T takes K rows straight from HBM into the A
+//     fragment (16-byte loads), and O^T = V^T * P^T reads V^T from a wave-private
+//     LDS tile that the wave fills with a register transpose.
+//   * Online softmax is fp32 in log2 units (exp2 with sm_scale * log2(e) folded in).
+#include "common.h"
+
+namespace fi {
+
+namespace decode {
+
+constexpr int kWaves = 4;                        // waves per workgroup
+constexpr int kIterTokens = 32;                  // tokens per wave per iteration
+constexpr int kWgTokens = kWaves * kIterTokens;  // tokens per workgroup iteration
+constexpr int kVtStride = kIterTokens + 4;       // fp16 per V^T row in LDS (bank padding)
+constexpr int kVtHalfs = kHeadDim * kVtStride;   // one wave's V^T tile
+constexpr int kMaxHeadsPerWg = 16;               // MFMA N dimension
+constexpr int kCmbStride = kHeadDim + 4;         // floats per merged row (bank padding)
+constexpr int kSmemBytes = kWaves * kVtHalfs * 2;
+
+static_assert(kWaves * kMaxHeadsPerWg * kCmbStride * 4 + kWaves * kMaxHeadsPerWg * 2 * 4 <=
+                  kSmemBytes,
+              "merge area must fit in the V^T tiles");
+
+struct Params {
+  const half_t* q;
+  int64_t q_sb, q_sh;
+  const half_t* k_cache;
+  const half_t* v_cache;
+  int64_t num_pool_blocks;
+  int block_size;
+  int num_kv_heads;
+  const int32_t* block_table;
+  int64_t bt_stride;
+  int max_blocks_per_seq;
+  const int32_t* context_lens;
+  int num_tokens;
+  half_t* o;
+  int64_t o_sb, o_sh;
+  int num_q_heads;
+  int group;         // query heads per kv head
+  int heads_per_wg;  // query heads served by one workgroup (divides group, <= 16)
+  float scale_log2;  // sm_scale * log2(e)
+  int tokens_per_split;
+  int max_splits;
+  float* part_o;   // [batch][num_q_heads][max_splits][128]
+  float* part_ml;  // [batch][num_q_heads][max_splits][2]
+  int direct;      // 1 -> a single partition, write o
+};
+
+__device__ __forceinline__ int row_context(const Params& p, int b) {
+  int ctx = p.context_lens ? p.context_lens[b] : p.num_tokens;
+  ctx = ctx < p.num_tokens ? ctx : p.num_tokens;
+  const int cap = p.max_blocks_per_seq * p.block_size;
+  ctx = ctx < cap ? ctx : cap;
+  return ctx < 0 ? 0 : ctx;
+}
+
+// Physical block holding logical token `tok` of row b, or -1 when the entry is
+// outside the pool (such tokens are treated as masked).
+__device__ __forceinline__ int64_t phys_block(const Params& p, int b, int tok) {
+  const int64_t e = p.block_table[(int64_t)b * p.bt_stride + tok / p.block_size];
+  return (e >= 0 && e < p.num_pool_blocks) ? e : -1;
+}
+
+__global__ __launch_bounds__(256) void partition_kernel(Params p) {
+  __shared__ __attribute__((aligned(16))) char smem[kSmemBytes];
+
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int col = lane & 15;  // MFMA column: query head within the workgroup
+  const int g = lane >> 4;    // 16-lane row of the wave
+  const int hgroups_per_kv = p.group / p.heads_per_wg;
+  const int kvh = blockIdx.x / hgroups_per_kv;
+  const int head0 = kvh * p.group + (blockIdx.x % hgroups_per_kv) * p.heads_per_wg;
+  const int split = blockIdx.y;
+  const int b = blockIdx.z;
+
+  const int ctx = row_context(p, b);
+  const int split_start = split * p.tokens_per_split;
+  if (!p.direct && split_start >= ctx) return;  // no tokens here; the merge skips it
+  const int split_end = min(split_start + p.tokens_per_split, ctx);
+
+  // Q^T fragments (B operand of S^T = K * Q^T): column `col` is query head head0+col;
+  // MFMA i takes head_dim d = 32*i + 8*g + s in reduction slot 8*g + s (the K
+  // fragment below uses the same map, so lanes g = 0..3 read 64 contiguous bytes).
+  half8 qf[4];
+  {
+    const bool valid = col < p.heads_per_wg;
+    const half_t* qrow = p.q + (int64_t)b * p.q_sb + (int64_t)(head0 + (valid ? col : 0)) * p.q_sh;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (valid) v = *(const u32x4*)(qrow + 32 * i + 8 * g);
+      qf[i] = as_half8(v);
+    }
+  }
+
+  const int64_t row_stride = (int64_t)p.num_kv_heads * kHeadDim;  // one pool slot
+  const half_t* kbase = p.k_cache + (int64_t)kvh * kHeadDim;
+  const half_t* vbase = p.v_cache + (int64_t)kvh * kHeadDim;
+  half_t* vt = (half_t*)smem + w * kVtHalfs;  // this wave's V^T tile [128][kVtStride]
+
+  // V loader lane roles: 8 head_dim values (dc) of 4 consecutive keys (kq).
+  const int dc = lane >> 2;
+  const int kq = lane & 3;
+
+  float m_run = kNegBig;
+  float l_run = 0.f;
+  floatx4 acc[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) acc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  for (int base = split_start + w * kIterTokens; base < split_end; base += kWgTokens) {
+    // ---- global loads: K fragments and V rows of 32 tokens (two 16-token tiles).
+    u32x4 kf[2][4];
+    u32x4 vr[2][4];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int tile = base + 16 * t;  // 16-token tiles never straddle a block
+      const int64_t phys = tile < split_end ? phys_block(p, b, tile) : -1;
+      const int64_t slot0 = (phys < 0 ? 0 : phys) * p.block_size + tile % p.block_size;
+      const bool kval = phys >= 0 && tile + col < split_end;
+      const half_t* krow = kbase + (slot0 + col) * row_stride;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        kf[t][i] = kval ? *(const u32x4*)(krow + 32 * i + 8 * g) : u32x4{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int vtok = tile + 4 * kq + j;
+        const bool vval = phys >= 0 && vtok < split_end;
+        const half_t* vrow = vbase + (slot0 + 4 * kq + j) * row_stride;
+        vr[t][j] = vval ? *(const u32x4*)(vrow + 8 * dc) : u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+
+    // ---- S^T = K * Q^T for the two tiles: lane holds keys 16t + 4g + r, column col.
+    floatx4 s[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      floatx4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        c = mfma16x16x32(as_half8(kf[t][i]), qf[i], c);
+      }
+      s[t] = c;
+    }
+
+    // ---- online softmax (log2 domain), masked keys -> -inf.
+    float tmax = kNegBig;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int tok = base + 16 * t + 4 * g + r;
+        const float x = tok < split_end ? s[t][r] * p.scale_log2 : -__builtin_inff();
+        s[t][r] = x;
+        tmax = fmaxf(tmax, x);
+      }
+    }
+    tmax = row4_max(tmax);
+    const float m_new = fmaxf(m_run, tmax);
+    const float alpha = fast_exp2(m_run - m_new);
+    m_run = m_new;
+    float psum = 0.f;
+    half8 pf;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float e = fast_exp2(s[t][r] - m_new);
+        psum += e;
+        pf[4 * t + r] = (half_t)e;
+      }
+    }
+    l_run = l_run * alpha + psum;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
+
+    // ---- V^T into this wave's LDS tile: lane writes rows d = 8*dc + e, keys 16t + 4kq..+3.
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int e2 = 0; e2 < 4; ++e2) {
+        // dword e2 of each key row holds d = 8*dc + 2*e2 (low) and + 1 (high)
+        const u32x2 lo = {pack_lo(vr[t][0][e2], vr[t][1][e2]), pack_lo(vr[t][2][e2], vr[t][3][e2])};
+        const u32x2 hi = {pack_hi(vr[t][0][e2], vr[t][1][e2]), pack_hi(vr[t][2][e2], vr[t][3][e2])};
+        *(u32x2*)(vt + (8 * dc + 2 * e2) * kVtStride + 16 * t + 4 * kq) = lo;
+        *(u32x2*)(vt + (8 * dc + 2 * e2 + 1) * kVtStride + 16 * t + 4 * kq) = hi;
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---- O^T += V^T * P^T: A = V^T rows d, slots (keys 4g..4g+3, 16+4g..16+4g+3).
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const half_t* row = vt + (16 * dt + col) * kVtStride;
+      const u32x2 a0 = *(const u32x2*)(row + 4 * g);
+      const u32x2 a1 = *(const u32x2*)(row + 16 + 4 * g);
+      const u32x4 a = {a0[0], a0[1], a1[0], a1[1]};
+      acc[dt] = mfma16x16x32(as_half8(a), pf, acc[dt]);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+
+  l_run = row4_sum(l_run);
+
+  // ---- merge the four waves through LDS (reuses the V^T area).
+  __syncthreads();
+  float* cmb_o = (float*)smem;                                   // [w][col][kCmbStride]
+  float* cmb_ml = cmb_o + kWaves * kMaxHeadsPerWg * kCmbStride;  // [w][col][2]
+  if (col < p.heads_per_wg) {
+    float* dst = cmb_o + (w * kMaxHeadsPerWg + col) * kCmbStride + 4 * g;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) *(floatx4*)(dst + 16 * dt) = acc[dt];
+    if (g == 0) {
+      cmb_ml[(w * kMaxHeadsPerWg + col) * 2 + 0] = m_run;
+      cmb_ml[(w * kMaxHeadsPerWg + col) * 2 + 1] = l_run;
+    }
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < p.heads_per_wg * kHeadDim; idx += blockDim.x) {
+    const int c = idx / kHeadDim;
+    const int d = idx % kHeadDim;
+    float mw[kWaves];
+    float mx = kNegBig;
+#pragma unroll
+    for (int ww = 0; ww < kWaves; ++ww) {
+      mw[ww] = cmb_ml[(ww * kMaxHeadsPerWg + c) * 2];
+      mx = fmaxf(mx, mw[ww]);
+    }
+    float L = 0.f, O = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < kWaves; ++ww) {
+      const float sc = fast_exp2(mw[ww] - mx);
+      L += sc * cmb_ml[(ww * kMaxHeadsPerWg + c) * 2 + 1];
+      O += sc * cmb_o[(ww * kMaxHeadsPerWg + c) * kCmbStride + d];
+    }
+    const int h = head0 + c;
+    if (p.direct) {
+      p.o[(int64_t)b * p.o_sb + (int64_t)h * p.o_sh + d] = (half_t)(L > 0.f ? O / L : 0.f);
+    } else {
+      const int64_t slot = ((int64_t)b * p.num_q_heads + h) * p.max_splits + split;
+      p.part_o[slot * kHeadDim + d] = O;
+      if (d == 0) {
+        p.part_ml[slot * 2 + 0] = mx;
+        p.part_ml[slot * 2 + 1] = L;
+      }
+    }
+  }
+}
+
+// Merge the partition partials of one (row, query head): o = sum_s e^(m_s-M) o_s /
+// sum_s e^(m_s-M) l_s, zeros for an empty row.
+__global__ __launch_bounds__(kHeadDim) void merge_kernel(Params p) {
+  const int h = blockIdx.x;
+  const int b = blockIdx.y;
+  const int d = threadIdx.x;
+  const int ctx = row_context(p, b);
+  const int nsplit = (ctx + p.tokens_per_split - 1) / p.tokens_per_split;
+  const int64_t slot0 = ((int64_t)b * p.num_q_heads + h) * p.max_splits;
+  float mx = kNegBig;
+  for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, p.part_ml[(slot0 + s) * 2]);
+  float L = 0.f, O = 0.f;
+  for (int s = 0; s < nsplit; ++s) {
+    const float sc = fast_exp2(p.part_ml[(slot0 + s) * 2] - mx);
+    L += sc * p.part_ml[(slot0 + s) * 2 + 1];
+    O += sc * p.part_o[(slot0 + s) * kHeadDim + d];
+  }
+  p.o[(int64_t)b * p.o_sb + (int64_t)h * p.o_sh + d] = (half_t)(L > 0.f ? O / L : 0.f);
+}
+
+// Partition size (tokens, a multiple of kWgTokens) for a call.  Aims for about 2048
+// workgroups so the 256 CUs stay busy at small batch; a context that fits in four
+// workgroup iterations is served by one partition and no merge.
+static int tokens_per_split(int64_t batch, int64_t wg_per_row, int64_t num_tokens) {
+  static int env_tps = -1;
+  if (env_tps < 0) {
+    const char* s = getenv("FI_DECODE_TOKENS_PER_SPLIT");
+    env_tps = s ? atoi(s) : 0;
+    if (env_tps < 0) env_tps = 0;
+  }
+  int64_t tps;
+  if (env_tps > 0) {
+    tps = env_tps;
+  } else if (num_tokens <= 4 * kWgTokens) {
+    tps = num_tokens;
+  } else {
+    const int64_t per_row = batch * wg_per_row;
+    int64_t want = (2048 + per_row - 1) / per_row;
+    if (want < 1) want = 1;
+    tps = (num_tokens + want - 1) / want;
+  }
+  tps = (tps + kWgTokens - 1) / kWgTokens * kWgTokens;
+  if (tps < kWgTokens) tps = kWgTokens;
+  return (int)tps;
+}
+
+static int heads_per_wg(int64_t group) {
+  for (int h = kMaxHeadsPerWg; h >= 1; --h)
+    if (group % h == 0) return h;
+  return 1;
+}
+
+}  // namespace decode
+}  // namespace fi
+
+extern "C" size_t fi_paged_attention_workspace_size(int64_t batch, int64_t num_q_heads,
+                                                    int64_t num_kv_heads,
+                                                    int64_t max_num_tokens, int64_t head_dim) {
+  using namespace fi::decode;
+  if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || max_num_tokens <= 0 ||
+      head_dim != fi::kHeadDim || num_q_heads % num_kv_heads != 0)
+    return 0;
+  const int64_t group = num_q_heads / num_kv_heads;
+  const int64_t wg_per_row = num_kv_heads * (group / heads_per_wg(group));
+  const int64_t tps = tokens_per_split(batch, wg_per_row, max_num_tokens);
+  const int64_t splits = (max_num_tokens + tps - 1) / tps;
+  if (splits <= 1) return 0;
+  return (size_t)(batch * num_q_heads * splits * (fi::kHeadDim + 2) * sizeof(float));
+}
+
+extern "C" int fi_paged_attention_fwd(const void* q, int64_t q_sb, int64_t q_sh,
+                                      const void* k_cache, const void* v_cache,
+                                      int64_t num_pool_blocks, int64_t block_size,
+                                      int64_t num_kv_heads, const int32_t* block_table,
+                                      int64_t bt_stride, int64_t max_blocks_per_seq,
+                                      const int32_t* context_lens, int64_t num_tokens, void* o,
+                                      int64_t o_sb, int64_t o_sh, int64_t batch,
+                                      int64_t num_q_heads, int64_t head_dim, float sm_scale,
+                                      void* workspace, size_t workspace_bytes, void* stream) {
+  using namespace fi;
+  using namespace fi::decode;
+  clear_error();
+  if (head_dim != kHeadDim) {
+    set_error("fi_paged_attention_fwd: head_dim %lld not supported (only %d)",
+              (long long)head_dim, kHeadDim);
+    return FI_ERR_UNSUPPORTED;
+  }
+  if (batch < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || num_tokens < 0 ||
+      num_pool_blocks < 0 || max_blocks_per_seq < 0 || num_q_heads % num_kv_heads != 0) {
+    set_error("fi_paged_attention_fwd: invalid sizes (batch %lld, heads %lld/%lld, tokens %lld)",
+              (long long)batch, (long long)num_q_heads, (long long)num_kv_heads,
+              (long long)num_tokens);
+    return FI_ERR_INVALID;
+  }
+  if (block_size <= 0 || block_size % 16 != 0) {
+    set_error("fi_paged_attention_fwd: block_size %lld must be a positive multiple of 16",
+              (long long)block_size);
+    return FI_ERR_UNSUPPORTED;
+  }
+  if (batch == 0) return FI_OK;
+  if (num_tokens > (int64_t)1 << 30 || num_pool_blocks * block_size * num_kv_heads > ((int64_t)1 << 40)) {
+    set_error("fi_paged_attention_fwd: sizes too large");
+    return FI_ERR_INVALID;
+  }
+  if (!q || !k_cache || !v_cache || !o || (!block_table && num_tokens > 0)) {
+    set_error("fi_paged_attention_fwd: null pointer");
+    return FI_ERR_INVALID;
+  }
+  if (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) & 15u ||
+      (q_sb | q_sh) % 8 != 0) {
+    set_error("fi_paged_attention_fwd: q and the pools must be 16-byte aligned");
+    return FI_ERR_INVALID;
+  }
+
+  const int64_t group = num_q_heads / num_kv_heads;
+  Params p;
+  p.q = (const half_t*)q;
+  p.q_sb = q_sb;
+  p.q_sh = q_sh;
+  p.k_cache = (const half_t*)k_cache;
+  p.v_cache = (const half_t*)v_cache;
+  p.num_pool_blocks = num_pool_blocks;
+  p.block_size = (int)block_size;
+  p.num_kv_heads = (int)num_kv_heads;
+  p.block_table = block_table;
+  p.bt_stride = bt_stride;
+  p.max_blocks_per_seq = (int)max_blocks_per_seq;
+  p.context_lens = context_lens;
+  p.num_tokens = (int)num_tokens;
+  p.o = (half_t*)o;
+  p.o_sb = o_sb;
+  p.o_sh = o_sh;
+  p.num_q_heads = (int)num_q_heads;
+  p.group = (int)group;
+  p.heads_per_wg = heads_per_wg(group);
+  p.scale_log2 = sm_scale * kLog2e;
+  const int64_t wg_per_row = num_kv_heads * (group / p.heads_per_wg);
+  p.tokens_per_split = tokens_per_split(batch, wg_per_row, num_tokens > 0 ? num_tokens : 1);
+  int64_t splits = (num_tokens + p.tokens_per_split - 1) / p.tokens_per_split;
+  if (splits < 1) splits = 1;
+  p.max_splits = (int)splits;
+  p.direct = splits == 1;
+  p.part_o = nullptr;
+  p.part_ml = nullptr;
+  if (!p.direct) {
+    const size_t need =
+        fi_paged_attention_workspace_size(batch, num_q_heads, num_kv_heads, num_tokens, head_dim);
+    if (!workspace || workspace_bytes < need) {
+      set_error("fi_paged_attention_fwd: workspace of %zu bytes needed, %zu given", need,
+                workspace ? workspace_bytes : (size_t)0);
+      return FI_ERR_WORKSPACE;
+    }
+    p.part_o = (float*)workspace;
+    p.part_ml = p.part_o + batch * num_q_heads * splits * kHeadDim;
+  }
+  if (batch > 65535 || splits > 65535) {
+    set_error("fi_paged_attention_fwd: grid too large");
+    return FI_ERR_UNSUPPORTED;
+  }
+  hipLaunchKernelGGL(partition_kernel, dim3((unsigned)wg_per_row, (unsigned)splits, (unsigned)batch),
+                     dim3(kWaves * 64), 0, (hipStream_t)stream, p);
+  int rc = check_launch("fi_paged_attention_fwd(partition)");
+  if (rc != FI_OK || p.direct) return rc;
+  hipLaunchKernelGGL(merge_kernel, dim3((unsigned)num_q_heads, (unsigned)batch), dim3(kHeadDim), 0,
+                     (hipStream_t)stream, p);
+  return check_launch("fi_paged_attention_fwd(merge)");
+}

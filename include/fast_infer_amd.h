@@ -1,0 +1,170 @@
+/*
+ * fast_infer_amd — C ABI of the MI355X (gfx950) attention hot path.
+ *
+ * Three device operations, each a drop-in for one piece of Fast_Infer's
+ * attention path:
+ *
+ *   fi_flash_attention_fwd   causal prefill attention
+ *                            replaces kernels/attention.py:80-113 (flash_attention,
+ *                            launching _flash_attn_fwd :8-77); with a non-null
+ *                            pool it also performs the prefill K/V write of
+ *                            model.py:162-183 (_store_kv_prefill) in the same pass.
+ *   fi_paged_attention_fwd   single-query attention over the paged KV pool
+ *                            replaces kernels/attention.py:191-233 (paged_attention,
+ *                            launching _paged_attention_kernel :116-188).
+ *   fi_kv_store              scatter of K/V rows into the paged pool
+ *                            replaces model.py:162-183 (_store_kv_prefill copies),
+ *                            model.py:185-201 (_store_kv_decode copies) and
+ *                            kv_cache.py:69-103 (KVCache.store / store_batch).
+ *
+ * Conventions shared by every entry point:
+ *   - Pointers are device pointers; sizes and strides are int64 and counted in
+ *     elements (not bytes).  The innermost (head_dim) stride is always 1.
+ *   - K/V pools are dense fp16 tensors [num_blocks, block_size, num_kv_heads,
+ *     head_dim] (the per-layer slice of kv_cache.py:25-28).
+ *   - Block tables are int32 [batch, max_blocks_per_seq] with a row stride;
+ *     -1 marks an unallocated entry (kv_cache.py:33-34).  Entries outside
+ *     [0, num_blocks) are never dereferenced: rows that map there are skipped.
+ *   - `stream` is a hipStream_t (NULL = the legacy default stream).  Every call
+ *     is asynchronous: it enqueues work and returns; nothing synchronises.
+ *   - The library keeps no mutable global state; calls are reentrant.
+ *   - Return value: FI_OK or an FI_ERR_* code; fi_last_error() then gives a
+ *     message for the calling thread.
+ *   - Only head_dim == 128 and fp16 data are implemented (the shapes of
+ *     Llama-3.2-3B, config.py:12-15).  Other head dims return
+ *     FI_ERR_UNSUPPORTED.
+ */
+#ifndef FAST_INFER_AMD_H
+#define FAST_INFER_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#if defined(__GNUC__) || defined(__clang__)
+#define FI_API __attribute__((visibility("default")))
+#else
+#define FI_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FI_OK 0
+#define FI_ERR_INVALID 1     /* bad shape, stride, alignment or null pointer */
+#define FI_ERR_UNSUPPORTED 2 /* valid request outside the implemented shapes */
+#define FI_ERR_HIP 3         /* the HIP runtime reported a launch error */
+#define FI_ERR_WORKSPACE 4   /* workspace missing or too small */
+
+/* Library ABI version (major * 100 + minor). */
+FI_API int fi_version(void);
+
+/* Message describing the last failing call made by this thread ("" if none). */
+FI_API const char* fi_last_error(void);
+
+/*
+ * Causal prefill attention, GQA-native.
+ * Replaces flash_attention(q, k, v, sm_scale) at kernels/attention.py:80-113.
+ *
+ *   q, o : [batch, num_q_heads,  seq_len, head_dim] with strides (q_sb, q_sh, q_ss)
+ *   k, v : [batch, num_kv_heads, seq_len, head_dim] with strides (k_sb, k_sh, k_ss)
+ *   num_q_heads % num_kv_heads == 0; query head h reads kv head h / (num_q_heads/num_kv_heads)
+ *   (the reference expands K/V with repeat_interleave, model.py:110-111; passing the
+ *   expanded K/V with num_kv_heads == num_q_heads gives the identical result).
+ *   Query row m attends to key rows n <= m (kernels/attention.py:57-58).
+ *   Rows must be 16-byte aligned: every stride a multiple of 8, pointers 16-byte aligned.
+ *
+ * Optional fused pool write (k_cache != NULL): additionally copies k[b, :, t, :] and
+ * v[b, :, t, :] into k_cache/v_cache at block block_table[b, t / block_size], slot
+ * t % block_size, for every t < seq_len — the write of model.py:176-183.  The fused
+ * path needs block_size == 64; other block sizes return FI_ERR_UNSUPPORTED (use
+ * fi_kv_store).  Table entries outside [0, num_pool_blocks) are skipped.
+ */
+FI_API int fi_flash_attention_fwd(const void* q, const void* k, const void* v, void* o,
+                           int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                           int64_t seq_len, int64_t head_dim,
+                           int64_t q_sb, int64_t q_sh, int64_t q_ss,
+                           int64_t k_sb, int64_t k_sh, int64_t k_ss,
+                           int64_t v_sb, int64_t v_sh, int64_t v_ss,
+                           int64_t o_sb, int64_t o_sh, int64_t o_ss,
+                           float sm_scale,
+                           void* k_cache, void* v_cache, int64_t num_pool_blocks,
+                           int64_t block_size, const int32_t* block_table,
+                           int64_t bt_stride, int64_t max_blocks_per_seq,
+                           void* stream);
+
+/*
+ * Bytes of device workspace fi_paged_attention_fwd needs for these sizes
+ * (0 when the call is served by a single pass).  `max_num_tokens` is the bound
+ * later passed as `num_tokens`.
+ */
+FI_API size_t fi_paged_attention_workspace_size(int64_t batch, int64_t num_q_heads,
+                                         int64_t num_kv_heads, int64_t max_num_tokens,
+                                         int64_t head_dim);
+
+/*
+ * Paged-attention decode (one query token per sequence), split-K over the context.
+ * Replaces paged_attention(q, k_cache, v_cache, block_table, block_size, num_tokens,
+ * sm_scale) at kernels/attention.py:191-233.
+ *
+ *   q, o        : [batch, num_q_heads, head_dim], strides (q_sb, q_sh) / (o_sb, o_sh)
+ *   k/v_cache   : [num_pool_blocks, block_size, num_kv_heads, head_dim], dense
+ *   block_table : int32, row b at block_table + b * bt_stride, max_blocks_per_seq entries
+ *   context_lens: NULL -> every row attends to its first num_tokens tokens (the
+ *                 reference's single shared length, kernels/attention.py:158-160);
+ *                 else int32[batch] per-row lengths, each clamped to num_tokens, so
+ *                 num_tokens must be >= max(context_lens).
+ *   Rows whose length is 0 produce zeros (kernels/attention.py:205-206).
+ *   block_size must be a multiple of 16.  workspace must hold
+ *   fi_paged_attention_workspace_size(batch, num_q_heads, num_kv_heads, num_tokens, head_dim)
+ *   bytes (it may be NULL when that is 0); its contents need no initialisation.
+ */
+FI_API int fi_paged_attention_fwd(const void* q, int64_t q_sb, int64_t q_sh,
+                           const void* k_cache, const void* v_cache,
+                           int64_t num_pool_blocks, int64_t block_size, int64_t num_kv_heads,
+                           const int32_t* block_table, int64_t bt_stride,
+                           int64_t max_blocks_per_seq,
+                           const int32_t* context_lens, int64_t num_tokens,
+                           void* o, int64_t o_sb, int64_t o_sh,
+                           int64_t batch, int64_t num_q_heads, int64_t head_dim,
+                           float sm_scale,
+                           void* workspace, size_t workspace_bytes,
+                           void* stream);
+
+/*
+ * Scatter K/V rows into the paged pool (byte-exact copies).
+ * Replaces the slice copies of model.py:176-183 (prefill), model.py:196-201 (decode)
+ * and kv_cache.py:69-103.
+ *
+ *   k, v : [batch, num_tokens, num_kv_heads, head_dim] with strides
+ *          (k_sb, k_st, k_sh) / (v_sb, v_st, v_sh)
+ *   Token t of row b lands at position p = start + t where start is
+ *   start_pos_per_seq[b] if that pointer is non-null, else start_pos; the row goes to
+ *   block block_table[b, p / block_size], slot p % block_size.  Positions whose
+ *   logical block is >= max_blocks_per_seq or whose table entry is outside
+ *   [0, num_pool_blocks) are skipped.
+ */
+FI_API int fi_kv_store(const void* k, int64_t k_sb, int64_t k_st, int64_t k_sh,
+                const void* v, int64_t v_sb, int64_t v_st, int64_t v_sh,
+                void* k_cache, void* v_cache, int64_t num_pool_blocks,
+                int64_t block_size, int64_t num_kv_heads, int64_t head_dim,
+                const int32_t* block_table, int64_t bt_stride, int64_t max_blocks_per_seq,
+                int64_t batch, int64_t num_tokens,
+                int64_t start_pos, const int32_t* start_pos_per_seq,
+                void* stream);
+
+/*
+ * Self-test of the gfx950 MFMA fragment layout the attention kernels assume
+ * (no counterpart in the reference; used by the test suite).  One wave computes
+ * C[16x16] = A[16x32] * B[32x16] with v_mfma_f32_16x16x32_f16, where lane l holds
+ * A[l % 16][8*(l/16) + s] and B[8*(l/16) + s][l % 16] for s = 0..7 and returns
+ * C[4*(l/16) + i][l % 16] for i = 0..3.
+ *   a, b: fp16 [64][8] (lane-major), c: fp32 [64][4] (lane-major).
+ */
+FI_API int fi_selftest_mfma_f16(const void* a, const void* b, void* c, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FAST_INFER_AMD_H */

@@ -1,0 +1,20 @@
+"""CPU oracle for the attention hot path — TEST INFRASTRUCTURE, never a product path.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may
+import, call, link or execute anything in this package, and only as the checker (or
+the timed CPU baseline) — the ``fast_infer_amd`` package never does.
+
+Contents (each function cites the reference file:line it restates):
+
+* ``attention`` — fp32 closed forms of causal GQA prefill and paged decode, and
+  numpy restatements of the reference's Triton tile loops (same tile sizes, same
+  online-softmax update order) for bit-level comparison with the reference's own
+  outputs.
+* ``kv`` — pure-Python restatement of the KV pool writes (model.py:162-201,
+  kv_cache.py:69-103) and of the block allocator (kv_cache.py:12-113).
+* ``ref_algo.c`` (+ ``native``) — the same tile algorithms in C with OpenMP, used
+  as the CPU baseline ("port").
+
+How each function is pinned (golden vectors from the reference kernels, closed
+forms, invariants, brute force) is listed in each module's docstring.
+"""

@@ -1,0 +1,118 @@
+"""The C-ABI library loads and exports every entry point of include/fast_infer_amd.h.
+
+CPU only: no call here launches a kernel.  The calls made return from argument
+validation before any HIP API is used, and check the error codes and messages.
+"""
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "fast_infer_amd.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fi_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from fast_infer_amd import _lib
+
+    if not _lib.LIB_PATH.exists():
+        pytest.fail(f"{_lib.LIB_PATH} is not built (run __graft_entry__.build())")
+    return _lib.load()
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    for n in ("fi_flash_attention_fwd", "fi_paged_attention_fwd", "fi_kv_store",
+              "fi_paged_attention_workspace_size", "fi_last_error", "fi_version"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    from fast_infer_amd import _lib
+
+    for name in _declared():
+        assert hasattr(lib, name), f"{name} missing from {_lib.LIB_PATH.name}"
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)],
+                         capture_output=True, text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    fi_exported = {s for s in exported if s.startswith("fi_")}
+    assert fi_exported == set(_declared()), "exports differ from the header"
+
+
+def test_version_and_empty_error(lib):
+    assert lib.fi_version() == 100
+    assert lib.fi_last_error() == b""
+
+
+def test_unsupported_head_dim(lib):
+    from fast_infer_amd import _lib
+
+    rc = lib.fi_paged_attention_fwd(8, 0, 0, 16, 16, 1, 64, 1, 16, 1, 1, None, 1, 32, 0, 0,
+                                    1, 1, 64, 1.0, None, 0, None)
+    assert rc == _lib.FI_ERR_UNSUPPORTED
+    assert b"head_dim 64" in lib.fi_last_error()
+    rc = lib.fi_flash_attention_fwd(16, 16, 16, 16, 1, 1, 1, 1, 96, *([8] * 12), 1.0,
+                                    None, None, 0, 64, None, 0, 0, None)
+    assert rc == _lib.FI_ERR_UNSUPPORTED
+    rc = lib.fi_kv_store(16, 8, 8, 8, 16, 8, 8, 8, 16, 16, 1, 64, 1, 80, 16, 1, 1, 1, 1, 0,
+                         None, None)
+    assert rc == _lib.FI_ERR_UNSUPPORTED
+
+
+def test_invalid_arguments(lib):
+    from fast_infer_amd import _lib
+
+    # heads not divisible
+    rc = lib.fi_flash_attention_fwd(16, 16, 16, 16, 1, 6, 4, 8, 128, *([8] * 12), 1.0,
+                                    None, None, 0, 64, None, 0, 0, None)
+    assert rc == _lib.FI_ERR_INVALID
+    # misaligned q pointer
+    rc = lib.fi_flash_attention_fwd(18, 16, 16, 16, 1, 8, 8, 8, 128, *([8] * 12), 1.0,
+                                    None, None, 0, 64, None, 0, 0, None)
+    assert rc == _lib.FI_ERR_INVALID and b"aligned" in lib.fi_last_error()
+    # fused pool write with another block size
+    rc = lib.fi_flash_attention_fwd(16, 16, 16, 16, 1, 8, 8, 8, 128, *([8] * 12), 1.0,
+                                    32, 32, 4, 32, 64, 4, 4, None)
+    assert rc == _lib.FI_ERR_UNSUPPORTED
+    # block size not a multiple of 16 for decode
+    rc = lib.fi_paged_attention_fwd(16, 8, 8, 16, 16, 1, 24, 1, 16, 1, 1, None, 1, 32, 8, 8,
+                                    1, 1, 128, 1.0, None, 0, None)
+    assert rc == _lib.FI_ERR_UNSUPPORTED
+    # null pools
+    rc = lib.fi_kv_store(16, 8, 8, 8, 16, 8, 8, 8, None, None, 1, 64, 1, 128, 16, 1, 1, 1, 1,
+                         0, None, None)
+    assert rc == _lib.FI_ERR_INVALID
+
+
+def test_empty_calls_are_noops(lib):
+    from fast_infer_amd import _lib
+
+    assert lib.fi_flash_attention_fwd(None, None, None, None, 0, 8, 8, 8, 128, *([8] * 12),
+                                      1.0, None, None, 0, 64, None, 0, 0, None) == _lib.FI_OK
+    assert lib.fi_kv_store(None, 8, 8, 8, None, 8, 8, 8, None, None, 1, 64, 1, 128, None, 1,
+                           1, 0, 5, 0, None, None) == _lib.FI_OK
+
+
+def test_workspace_size(lib):
+    # one partition (no workspace) for short contexts, partials for long ones
+    assert lib.fi_paged_attention_workspace_size(1, 24, 8, 256, 128) == 0
+    n = lib.fi_paged_attention_workspace_size(32, 24, 8, 4096, 128)
+    assert n > 0 and n % (32 * 24 * 130 * 4) == 0
+    assert lib.fi_paged_attention_workspace_size(32, 24, 8, 4096, 64) == 0
+    rc = lib.fi_paged_attention_fwd(16, 3072, 128, 16, 16, 2048, 64, 8, 16, 64, 64, None,
+                                    4096, 32, 3072, 128, 32, 24, 128, 1.0, None, 0, None)
+    from fast_infer_amd import _lib
+
+    assert rc == _lib.FI_ERR_WORKSPACE
+    assert ctypes.c_size_t(n).value == n
