@@ -126,10 +126,12 @@ __global__ __launch_bounds__(256) void partition_kernel(Params p) {
     // ---- global loads: K fragments and V rows of 32 tokens (two 16-token tiles).
     u32x4 kf[2][4];
     u32x4 vr[2][4];
+    bool tile_ok[2];  // false: past the partition or a table entry outside the pool
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const int tile = base + 16 * t;  // 16-token tiles never straddle a block
       const int64_t phys = tile < split_end ? phys_block(p, b, tile) : -1;
+      tile_ok[t] = phys >= 0;
       const int64_t slot0 = (phys < 0 ? 0 : phys) * p.block_size + tile % p.block_size;
       const bool kval = phys >= 0 && tile + col < split_end;
       const half_t* krow = kbase + (slot0 + col) * row_stride;
@@ -158,14 +160,16 @@ __global__ __launch_bounds__(256) void partition_kernel(Params p) {
       s[t] = c;
     }
 
-    // ---- online softmax (log2 domain), masked keys -> -inf.
+    // ---- online softmax (log2 domain); tokens past the partition or in a tile whose
+    // table entry is outside the pool are masked to -inf.
     float tmax = kNegBig;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int tok = base + 16 * t + 4 * g + r;
-        const float x = tok < split_end ? s[t][r] * p.scale_log2 : -__builtin_inff();
+        const float x =
+            (tile_ok[t] && tok < split_end) ? s[t][r] * p.scale_log2 : -__builtin_inff();
         s[t][r] = x;
         tmax = fmaxf(tmax, x);
       }
