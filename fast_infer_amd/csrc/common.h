@@ -53,6 +53,14 @@ __device__ __forceinline__ float row4_sum(float x) {
   return x;
 }
 
+// Order this wave's LDS writes before its later LDS reads (and reads before later
+// writes) when lanes exchange data through LDS within one wave.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Pack two fp16 values (given as the low/high 16 bits of two dwords) into one dword.
 __device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t b) {
   return (a & 0xffffu) | (b << 16);

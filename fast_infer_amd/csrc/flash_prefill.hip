@@ -130,7 +130,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(Params p) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int w = tid >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index (uniform)
   const int col = lane & 15;
   const int g = lane >> 4;
   const int dc = lane >> 2;  // V loader: 8 head_dim values

@@ -28,6 +28,11 @@ constexpr int kVtHalfs = kHeadDim * kVtStride;   // one wave's V^T tile
 constexpr int kMaxHeadsPerWg = 16;               // MFMA N dimension
 constexpr int kCmbStride = kHeadDim + 4;         // floats per merged row (bank padding)
 constexpr int kSmemBytes = kWaves * kVtHalfs * 2;
+constexpr int kMaxSplitTokens = 4096;                       // cap on the partition size
+constexpr int kMaxSplitEntries = kMaxSplitTokens / 16 + 1;  // table entries of a partition
+constexpr int kMaxSplits = 1024;                            // partitions per row
+constexpr int kOutOfRange = 0x40000000;  // buffer offset beyond any block: loads return 0
+constexpr int kBufferWord3 = 0x00020000;  // raw buffer: 32-bit data format, no swizzle
 
 static_assert(kWaves * kMaxHeadsPerWg * kCmbStride * 4 + kWaves * kMaxHeadsPerWg * 2 * 4 <=
                   kSmemBytes,
@@ -67,18 +72,130 @@ __device__ __forceinline__ int row_context(const Params& p, int b) {
   return ctx < 0 ? 0 : ctx;
 }
 
-// Physical block holding logical token `tok` of row b, or -1 when the entry is
-// outside the pool (such tokens are treated as masked).
-__device__ __forceinline__ int64_t phys_block(const Params& p, int b, int tok) {
-  const int64_t e = p.block_table[(int64_t)b * p.bt_stride + tok / p.block_size];
-  return (e >= 0 && e < p.num_pool_blocks) ? e : -1;
+// Registers of one wave iteration: 32 tokens as two 16-token tiles.
+struct IterRegs {
+  u32x4 kf[2][4];  // K A-fragments: lane (col, g) holds token tile+col, d = 32i + 8g..+7
+  u32x4 vr[2][4];  // V rows: lane (dc, kq) holds token tile + 4kq + j, d = 8dc..8dc+7
+  bool ok[2];      // tile inside the partition and mapped to a pool block
+};
+
+// Buffer descriptor covering one kv head's rows of one pool block; a block outside the
+// pool gets zero records, so every load through it returns 0 without touching memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t block_rsrc(const half_t* pool, int64_t phys,
+                                                            int64_t block_bytes, int kv_off) {
+  const bool ok = phys >= 0;
+  const char* base = (const char*)pool + (ok ? phys * block_bytes : 0) + kv_off;
+  return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0,
+                                           ok ? (int)(block_bytes - kv_off) : 0, kBufferWord3);
 }
 
-__global__ __launch_bounds__(256) void partition_kernel(Params p) {
+// Issue the global loads of the wave iteration starting at token `base`.  Lanes whose
+// token is outside [.., split_end) get an out-of-range offset and read zeros.
+__device__ __forceinline__ void issue_iter(const Params& p, const int* s_tab, int tab0,
+                                           int base, int split_end, int kv_off,
+                                           int64_t block_bytes, int row_bytes, int col, int g,
+                                           int dc, int kq, IterRegs& r) {
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int tile = base + 16 * t;  // 16-token tiles never straddle a block
+    int64_t phys = -1;
+    if (tile < split_end) phys = __builtin_amdgcn_readfirstlane(s_tab[tile / p.block_size - tab0]);
+    r.ok[t] = phys >= 0;
+    const __amdgpu_buffer_rsrc_t kr = block_rsrc(p.k_cache, phys, block_bytes, kv_off);
+    const __amdgpu_buffer_rsrc_t vr = block_rsrc(p.v_cache, phys, block_bytes, kv_off);
+    const int slot = tile % p.block_size;
+    const int koff = tile + col < split_end ? (slot + col) * row_bytes + 16 * g : kOutOfRange;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      r.kf[t][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff + 64 * i, 0, 0));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int tok = 4 * kq + j;
+      const int voff = tile + tok < split_end ? (slot + tok) * row_bytes + 16 * dc : kOutOfRange;
+      r.vr[t][j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, voff, 0, 0));
+    }
+  }
+}
+
+// Online-softmax update of one wave iteration (32 tokens at `base`).
+__device__ __forceinline__ void consume_iter(const Params& p, const IterRegs& r, int base,
+                                             int split_end, const half8 (&qf)[4], half_t* vt,
+                                             int col, int g, int dc, int kq, float& m_run,
+                                             float& l_run, floatx4 (&acc)[8]) {
+  // S^T = K * Q^T for the two tiles: lane holds keys 16t + 4g + r of column col.
+  floatx4 s[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    floatx4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) c = mfma16x16x32(as_half8(r.kf[t][i]), qf[i], c);
+    s[t] = c;
+  }
+
+  // Online softmax (log2 domain); tokens past the partition or in a tile whose table
+  // entry is outside the pool are masked to -inf.
+  float tmax = kNegBig;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int tok = base + 16 * t + 4 * g + i;
+      const float x = (r.ok[t] && tok < split_end) ? s[t][i] * p.scale_log2 : -__builtin_inff();
+      s[t][i] = x;
+      tmax = fmaxf(tmax, x);
+    }
+  }
+  tmax = row4_max(tmax);
+  const float m_new = fmaxf(m_run, tmax);
+  const float alpha = fast_exp2(m_run - m_new);
+  m_run = m_new;
+  float psum = 0.f;
+  half8 pf;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float e = fast_exp2(s[t][i] - m_new);
+      psum += e;
+      pf[4 * t + i] = (half_t)e;
+    }
+  }
+  l_run = l_run * alpha + psum;
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
+
+  // V^T into this wave's LDS tile: lane writes rows d = 8dc + e, keys 16t + 4kq..+3.
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+#pragma unroll
+    for (int e2 = 0; e2 < 4; ++e2) {
+      // dword e2 of each key row holds d = 8dc + 2e2 (low half) and + 1 (high half)
+      const u32x2 lo = {pack_lo(r.vr[t][0][e2], r.vr[t][1][e2]), pack_lo(r.vr[t][2][e2], r.vr[t][3][e2])};
+      const u32x2 hi = {pack_hi(r.vr[t][0][e2], r.vr[t][1][e2]), pack_hi(r.vr[t][2][e2], r.vr[t][3][e2])};
+      *(u32x2*)(vt + (8 * dc + 2 * e2) * kVtStride + 16 * t + 4 * kq) = lo;
+      *(u32x2*)(vt + (8 * dc + 2 * e2 + 1) * kVtStride + 16 * t + 4 * kq) = hi;
+    }
+  }
+  wave_lds_sync();
+
+  // O^T += V^T * P^T: A = V^T rows d, slots (keys 4g..4g+3, 16+4g..16+4g+3).
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) {
+    const half_t* row = vt + (16 * dt + col) * kVtStride;
+    const u32x2 a0 = *(const u32x2*)(row + 4 * g);
+    const u32x2 a1 = *(const u32x2*)(row + 16 + 4 * g);
+    const u32x4 a = {a0[0], a0[1], a1[0], a1[1]};
+    acc[dt] = mfma16x16x32(as_half8(a), pf, acc[dt]);
+  }
+  wave_lds_sync();
+}
+
+__global__ __launch_bounds__(256, 2) void partition_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) char smem[kSmemBytes];
+  __shared__ int s_tab[kMaxSplitEntries];
 
   const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave index (uniform)
   const int col = lane & 15;  // MFMA column: query head within the workgroup
   const int g = lane >> 4;    // 16-lane row of the wave
   const int hgroups_per_kv = p.group / p.heads_per_wg;
@@ -92,9 +209,19 @@ __global__ __launch_bounds__(256) void partition_kernel(Params p) {
   if (!p.direct && split_start >= ctx) return;  // no tokens here; the merge skips it
   const int split_end = min(split_start + p.tokens_per_split, ctx);
 
+  // Block-table entries of this partition, validated once, staged in LDS.
+  const int tab0 = split_start / p.block_size;
+  if (split_end > split_start) {
+    const int n_ent = (split_end - 1) / p.block_size - tab0 + 1;
+    for (int i = threadIdx.x; i < n_ent; i += blockDim.x) {
+      const int64_t e = p.block_table[(int64_t)b * p.bt_stride + tab0 + i];
+      s_tab[i] = (e >= 0 && e < p.num_pool_blocks) ? (int)e : -1;
+    }
+  }
+
   // Q^T fragments (B operand of S^T = K * Q^T): column `col` is query head head0+col;
   // MFMA i takes head_dim d = 32*i + 8*g + s in reduction slot 8*g + s (the K
-  // fragment below uses the same map, so lanes g = 0..3 read 64 contiguous bytes).
+  // fragment uses the same map, so lanes g = 0..3 read 64 contiguous bytes).
   half8 qf[4];
   {
     const bool valid = col < p.heads_per_wg;
@@ -106,15 +233,14 @@ __global__ __launch_bounds__(256) void partition_kernel(Params p) {
       qf[i] = as_half8(v);
     }
   }
+  __syncthreads();
 
-  const int64_t row_stride = (int64_t)p.num_kv_heads * kHeadDim;  // one pool slot
-  const half_t* kbase = p.k_cache + (int64_t)kvh * kHeadDim;
-  const half_t* vbase = p.v_cache + (int64_t)kvh * kHeadDim;
+  const int row_bytes = p.num_kv_heads * kHeadDim * 2;  // one pool slot, all kv heads
+  const int64_t block_bytes = (int64_t)p.block_size * row_bytes;
+  const int kv_off = kvh * kHeadDim * 2;
   half_t* vt = (half_t*)smem + w * kVtHalfs;  // this wave's V^T tile [128][kVtStride]
-
-  // V loader lane roles: 8 head_dim values (dc) of 4 consecutive keys (kq).
-  const int dc = lane >> 2;
-  const int kq = lane & 3;
+  const int dc = lane >> 2;  // V loader: 8 head_dim values
+  const int kq = lane & 3;   // V loader: 4 consecutive keys
 
   float m_run = kNegBig;
   float l_run = 0.f;
@@ -122,105 +248,22 @@ __global__ __launch_bounds__(256) void partition_kernel(Params p) {
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) acc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  for (int base = split_start + w * kIterTokens; base < split_end; base += kWgTokens) {
-    // ---- global loads: K fragments and V rows of 32 tokens (two 16-token tiles).
-    u32x4 kf[2][4];
-    u32x4 vr[2][4];
-    bool tile_ok[2];  // false: past the partition or a table entry outside the pool
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int tile = base + 16 * t;  // 16-token tiles never straddle a block
-      const int64_t phys = tile < split_end ? phys_block(p, b, tile) : -1;
-      tile_ok[t] = phys >= 0;
-      const int64_t slot0 = (phys < 0 ? 0 : phys) * p.block_size + tile % p.block_size;
-      const bool kval = phys >= 0 && tile + col < split_end;
-      const half_t* krow = kbase + (slot0 + col) * row_stride;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        kf[t][i] = kval ? *(const u32x4*)(krow + 32 * i + 8 * g) : u32x4{0u, 0u, 0u, 0u};
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int vtok = tile + 4 * kq + j;
-        const bool vval = phys >= 0 && vtok < split_end;
-        const half_t* vrow = vbase + (slot0 + 4 * kq + j) * row_stride;
-        vr[t][j] = vval ? *(const u32x4*)(vrow + 8 * dc) : u32x4{0u, 0u, 0u, 0u};
-      }
-    }
-
-    // ---- S^T = K * Q^T for the two tiles: lane holds keys 16t + 4g + r, column col.
-    floatx4 s[2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      floatx4 c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        c = mfma16x16x32(as_half8(kf[t][i]), qf[i], c);
-      }
-      s[t] = c;
-    }
-
-    // ---- online softmax (log2 domain); tokens past the partition or in a tile whose
-    // table entry is outside the pool are masked to -inf.
-    float tmax = kNegBig;
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int tok = base + 16 * t + 4 * g + r;
-        const float x =
-            (tile_ok[t] && tok < split_end) ? s[t][r] * p.scale_log2 : -__builtin_inff();
-        s[t][r] = x;
-        tmax = fmaxf(tmax, x);
-      }
-    }
-    tmax = row4_max(tmax);
-    const float m_new = fmaxf(m_run, tmax);
-    const float alpha = fast_exp2(m_run - m_new);
-    m_run = m_new;
-    float psum = 0.f;
-    half8 pf;
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float e = fast_exp2(s[t][r] - m_new);
-        psum += e;
-        pf[4 * t + r] = (half_t)e;
-      }
-    }
-    l_run = l_run * alpha + psum;
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
-
-    // ---- V^T into this wave's LDS tile: lane writes rows d = 8*dc + e, keys 16t + 4kq..+3.
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-#pragma unroll
-      for (int e2 = 0; e2 < 4; ++e2) {
-        // dword e2 of each key row holds d = 8*dc + 2*e2 (low) and + 1 (high)
-        const u32x2 lo = {pack_lo(vr[t][0][e2], vr[t][1][e2]), pack_lo(vr[t][2][e2], vr[t][3][e2])};
-        const u32x2 hi = {pack_hi(vr[t][0][e2], vr[t][1][e2]), pack_hi(vr[t][2][e2], vr[t][3][e2])};
-        *(u32x2*)(vt + (8 * dc + 2 * e2) * kVtStride + 16 * t + 4 * kq) = lo;
-        *(u32x2*)(vt + (8 * dc + 2 * e2 + 1) * kVtStride + 16 * t + 4 * kq) = hi;
-      }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-    // ---- O^T += V^T * P^T: A = V^T rows d, slots (keys 4g..4g+3, 16+4g..16+4g+3).
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const half_t* row = vt + (16 * dt + col) * kVtStride;
-      const u32x2 a0 = *(const u32x2*)(row + 4 * g);
-      const u32x2 a1 = *(const u32x2*)(row + 16 + 4 * g);
-      const u32x4 a = {a0[0], a0[1], a1[0], a1[1]};
-      acc[dt] = mfma16x16x32(as_half8(a), pf, acc[dt]);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // Two-deep software pipeline: the loads of iteration it+1 are in flight while
+  // iteration it is consumed.  Loads past the partition read zeros (no traffic).
+  const int first = split_start + w * kIterTokens;
+  const int n_it = first < split_end ? (split_end - first + kWgTokens - 1) / kWgTokens : 0;
+  IterRegs ra, rb;
+  if (n_it > 0)
+    issue_iter(p, s_tab, tab0, first, split_end, kv_off, block_bytes, row_bytes, col, g, dc, kq, ra);
+  for (int it = 0; it < n_it; it += 2) {
+    const int b0 = first + it * kWgTokens;
+    issue_iter(p, s_tab, tab0, b0 + kWgTokens, split_end, kv_off, block_bytes, row_bytes, col, g,
+               dc, kq, rb);
+    consume_iter(p, ra, b0, split_end, qf, vt, col, g, dc, kq, m_run, l_run, acc);
+    if (it + 1 >= n_it) break;
+    issue_iter(p, s_tab, tab0, b0 + 2 * kWgTokens, split_end, kv_off, block_bytes, row_bytes, col,
+               g, dc, kq, ra);
+    consume_iter(p, rb, b0 + kWgTokens, split_end, qf, vt, col, g, dc, kq, m_run, l_run, acc);
   }
 
   l_run = row4_sum(l_run);
@@ -271,28 +314,37 @@ __global__ __launch_bounds__(256) void partition_kernel(Params p) {
 }
 
 // Merge the partition partials of one (row, query head): o = sum_s e^(m_s-M) o_s /
-// sum_s e^(m_s-M) l_s, zeros for an empty row.
+// sum_s e^(m_s-M) l_s, zeros for an empty row.  The (m, l) pairs are staged in LDS
+// by all threads at once; the weighted sum over partitions then issues independent
+// loads per thread.
 __global__ __launch_bounds__(kHeadDim) void merge_kernel(Params p) {
+  __shared__ float s_w[kMaxSplits];
+  __shared__ float s_l[kMaxSplits];
   const int h = blockIdx.x;
   const int b = blockIdx.y;
   const int d = threadIdx.x;
   const int ctx = row_context(p, b);
   const int nsplit = (ctx + p.tokens_per_split - 1) / p.tokens_per_split;
   const int64_t slot0 = ((int64_t)b * p.num_q_heads + h) * p.max_splits;
-  float mx = kNegBig;
-  for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, p.part_ml[(slot0 + s) * 2]);
-  float L = 0.f, O = 0.f;
-  for (int s = 0; s < nsplit; ++s) {
-    const float sc = fast_exp2(p.part_ml[(slot0 + s) * 2] - mx);
-    L += sc * p.part_ml[(slot0 + s) * 2 + 1];
-    O += sc * p.part_o[(slot0 + s) * kHeadDim + d];
+  for (int s = d; s < nsplit; s += kHeadDim) {
+    s_w[s] = p.part_ml[(slot0 + s) * 2];
+    s_l[s] = p.part_ml[(slot0 + s) * 2 + 1];
   }
+  __syncthreads();
+  float mx = kNegBig;
+  for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, s_w[s]);
+  float L = 0.f;
+  for (int s = 0; s < nsplit; ++s) L += fast_exp2(s_w[s] - mx) * s_l[s];
+  float O = 0.f;
+#pragma unroll 8
+  for (int s = 0; s < nsplit; ++s) O += fast_exp2(s_w[s] - mx) * p.part_o[(slot0 + s) * kHeadDim + d];
   p.o[(int64_t)b * p.o_sb + (int64_t)h * p.o_sh + d] = (half_t)(L > 0.f ? O / L : 0.f);
 }
 
-// Partition size (tokens, a multiple of kWgTokens) for a call.  Aims for about 2048
-// workgroups so the 256 CUs stay busy at small batch; a context that fits in four
-// workgroup iterations is served by one partition and no merge.
+// Partition size (tokens, a multiple of kWgTokens, at most kMaxSplitTokens) for a call.
+// Aims for about kTargetWgs workgroups so the 256 CUs stay busy at small batch; a
+// context that fits in four workgroup iterations is served by one partition and no
+// merge.  FI_DECODE_TOKENS_PER_SPLIT overrides the choice (for tuning sweeps).
 static int tokens_per_split(int64_t batch, int64_t wg_per_row, int64_t num_tokens) {
   static int env_tps = -1;
   if (env_tps < 0) {
@@ -300,6 +352,13 @@ static int tokens_per_split(int64_t batch, int64_t wg_per_row, int64_t num_token
     env_tps = s ? atoi(s) : 0;
     if (env_tps < 0) env_tps = 0;
   }
+  static int env_target = -1;
+  if (env_target < 0) {
+    const char* s = getenv("FI_DECODE_TARGET_WGS");
+    env_target = s ? atoi(s) : 0;
+    if (env_target < 0) env_target = 0;
+  }
+  const int64_t target = env_target > 0 ? env_target : 2048;
   int64_t tps;
   if (env_tps > 0) {
     tps = env_tps;
@@ -307,12 +366,15 @@ static int tokens_per_split(int64_t batch, int64_t wg_per_row, int64_t num_token
     tps = num_tokens;
   } else {
     const int64_t per_row = batch * wg_per_row;
-    int64_t want = (2048 + per_row - 1) / per_row;
+    int64_t want = (target + per_row - 1) / per_row;
     if (want < 1) want = 1;
     tps = (num_tokens + want - 1) / want;
   }
+  const int64_t min_tps = (num_tokens + kMaxSplits - 1) / kMaxSplits;
+  if (tps < min_tps) tps = min_tps;
   tps = (tps + kWgTokens - 1) / kWgTokens * kWgTokens;
   if (tps < kWgTokens) tps = kWgTokens;
+  if (tps > kMaxSplitTokens) tps = kMaxSplitTokens;
   return (int)tps;
 }
 
@@ -370,9 +432,11 @@ extern "C" int fi_paged_attention_fwd(const void* q, int64_t q_sb, int64_t q_sh,
     return FI_ERR_UNSUPPORTED;
   }
   if (batch == 0) return FI_OK;
-  if (num_tokens > (int64_t)1 << 30 || num_pool_blocks * block_size * num_kv_heads > ((int64_t)1 << 40)) {
-    set_error("fi_paged_attention_fwd: sizes too large");
-    return FI_ERR_INVALID;
+  if (num_tokens > (int64_t)kMaxSplitTokens * kMaxSplits ||
+      block_size * num_kv_heads * kHeadDim * 2 > ((int64_t)1 << 30)) {
+    set_error("fi_paged_attention_fwd: num_tokens %lld or block bytes too large",
+              (long long)num_tokens);
+    return FI_ERR_UNSUPPORTED;
   }
   if (!q || !k_cache || !v_cache || !o || (!block_table && num_tokens > 0)) {
     set_error("fi_paged_attention_fwd: null pointer");

@@ -1,0 +1,37 @@
+"""MI355X roofline constants and the algorithmic work of the attention path.
+
+Peaks are MI355X's published dense figures for one GPU.  The work formulas count
+what the algorithm must move or compute, independent of how a kernel does it:
+
+* paged decode — every context token's K and V row of every kv head once (4 KiB per
+  token at 8 kv heads x 128 dims x fp16 x 2), plus q and o, plus the block-table
+  entries covering the context;
+* causal prefill — 4 * B * H * S^2 * D / 2 flops (QK^T and PV over the causal half).
+"""
+
+from __future__ import annotations
+
+import math
+
+HBM_PEAK_GBS = 8000.0            # HBM3E, GB/s
+FP16_MFMA_PEAK_TFLOPS = 2516.6   # dense fp16 MFMA, TFLOP/s (256 CU x 2.4 GHz x 4096 flop/clk)
+
+
+def decode_bytes(context_lens, num_q_heads: int, num_kv_heads: int, head_dim: int,
+                 block_size: int) -> int:
+    """Algorithmic HBM bytes of one decode call over rows with these context lengths."""
+    lens = [int(c) for c in context_lens]
+    kv = sum(lens) * num_kv_heads * head_dim * 2 * 2
+    qo = 2 * len(lens) * num_q_heads * head_dim * 2
+    table = 4 * sum(math.ceil(c / block_size) for c in lens)
+    return kv + qo + table
+
+
+def prefill_flops(batch: int, num_heads: int, seq_len: int, head_dim: int) -> float:
+    """Algorithmic flops of causal attention (QK^T + PV over the causal half)."""
+    return 4.0 * batch * num_heads * seq_len * seq_len * head_dim / 2.0
+
+
+def prefill_scatter_bytes(batch: int, seq_len: int, num_kv_heads: int, head_dim: int) -> int:
+    """Bytes the fused K/V pool write stores (K and V rows of every token)."""
+    return batch * seq_len * num_kv_heads * head_dim * 2 * 2
