@@ -22,17 +22,19 @@
 namespace fi {
 namespace prefill {
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;
+constexpr int kThreads = kWaves * 64;
 constexpr int kRowsPerWave = 16;                 // query positions per wave
-constexpr int kQTile = kWaves * kRowsPerWave;    // query positions per workgroup
-constexpr int kKTile = 64;                       // keys per K/V tile
-constexpr int kKStride = kHeadDim + 8;           // fp16 per K row in LDS (bank padding)
-constexpr int kVtStride = kKTile + 4;            // fp16 per V^T row in LDS (bank padding)
-constexpr int kKHalfs = kKTile * kKStride;
-constexpr int kVtHalfs = kHeadDim * kVtStride;
-constexpr int kStageHalfs = kKHalfs + kVtHalfs;  // one buffer stage
-constexpr int kSmemBytes = 2 * kStageHalfs * 2;
-static_assert(kQTile == kKTile, "the diagonal tile must coincide with the query tile");
+constexpr int kQTile = kWaves * kRowsPerWave;    // query positions per workgroup (128)
+constexpr int kKTile = 64;                       // keys per K/V tile (one pool block)
+constexpr int kRowBytes = kHeadDim * 2;          // one K or V row in LDS (256 bytes)
+constexpr int kTileBytes = kKTile * kRowBytes;   // 16 KiB
+constexpr int kStageBytes = 2 * kTileBytes;      // K tile + V tile
+constexpr int kRowsPerWaveLoad = kKTile / kWaves;  // K (and V) tile rows each wave loads
+constexpr int kChunks = kKTile * 16 / kThreads;     // 16-byte chunks of K (and V) per thread
+constexpr int kOutOfRange = 0x7ffffff0;          // buffer offset past any tensor: loads give 0
+constexpr int kBufferWord3 = 0x00020000;
+static_assert(kQTile % kKTile == 0, "query tiles cover whole key tiles");
 
 struct Params {
   const half_t* q;
@@ -45,11 +47,16 @@ struct Params {
   int64_t o_sb, o_sh, o_ss;
   int seq_len;
   int num_kv_heads;
-  int group;        // query heads per kv head
-  int hg_per_kv;    // workgroups per kv head (group / heads per workgroup)
-  float scale_log2; // sm_scale * log2(e)
+  int group;         // query heads per kv head
+  int hg_per_kv;     // workgroups per kv head (group / heads per workgroup)
+  float scale_log2;  // |sm_scale| * log2(e)
+  uint32_t q_sign;   // 0x80008000 when sm_scale < 0: Q is negated instead of the scale
   int num_q_tiles;
-  half_t* k_cache;  // optional pool (block_size 64)
+  int k_records;     // bytes addressable from one (batch, kv head) base of k
+  int v_records;
+  int k_row_bytes;   // k_ss * 2 (spans are checked to fit 31 bits)
+  int v_row_bytes;
+  half_t* k_cache;   // optional pool (block_size 64)
   half_t* v_cache;
   int64_t num_pool_blocks;
   const int32_t* block_table;
@@ -57,51 +64,47 @@ struct Params {
   int max_blocks_per_seq;
 };
 
-// Global->register staging of one 64-key K/V tile by the 256 threads of a workgroup.
-struct TileRegs {
-  u32x4 k[4];  // K chunk: key = k0 + (f >> 4), d = 8 * (f & 15), f = 256 * j + tid
-  u32x4 v[4];  // V rows: key = k0 + 16 * w + 4 * kq + j, d = 8 * dc..8 * dc + 7
-};
+// Byte address in a K or V LDS tile of 16-byte chunk c (0..15) of row r: rows are
+// 256 bytes, chunks XOR-swizzled by the row so that 16 consecutive rows read at one
+// column hit 16 different bank groups.
+__device__ __forceinline__ int swz(int r, int c) { return r * kRowBytes + ((c ^ (r & 15)) << 4); }
 
-__device__ __forceinline__ void load_tile(const Params& p, const half_t* kh, const half_t* vh,
-                                          int k0, int tid, int w, int dc, int kq, TileRegs& r) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int f = 256 * j + tid;
-    const int key = k0 + (f >> 4);
-    r.k[j] = key < p.seq_len ? *(const u32x4*)(kh + (int64_t)key * p.k_ss + 8 * (f & 15))
-                             : u32x4{0u, 0u, 0u, 0u};
-  }
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int key = k0 + 16 * w + 4 * kq + j;
-    r.v[j] = key < p.seq_len ? *(const u32x4*)(vh + (int64_t)key * p.v_ss + 8 * dc)
-                             : u32x4{0u, 0u, 0u, 0u};
-  }
+// Wait until at most `n` of this wave's vector-memory operations are outstanding
+// (vmcnt only; LDS and export counters untouched).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-__device__ __forceinline__ void store_tile(half_t* stage, int tid, int w, int dc, int kq,
-                                           const TileRegs& r) {
-  half_t* ks = stage;
-  half_t* vts = stage + kKHalfs;
+// Issue the direct-to-LDS loads of this wave's rows of the K/V tile at key k0 into
+// `stage` (K at +0, V at +kTileBytes).  One instruction moves 4 rows (64 lanes x 16
+// bytes) to 1 KiB of consecutive LDS; lane l fills swizzled position l%16 of row
+// 4q + l/16, so it fetches global chunk (l%16) ^ (row & 15).  Rows past seq_len, or a
+// tile past the end (k0 < 0), fetch zeros through the buffer bounds check.
+__device__ __forceinline__ void issue_tile(const Params& p, __amdgpu_buffer_rsrc_t kr,
+                                           __amdgpu_buffer_rsrc_t vr, char* stage, int k0,
+                                           int w, int lane) {
+  typedef void __attribute__((address_space(3))) lds_void;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int f = 256 * j + tid;
-    *(u32x4*)(ks + (f >> 4) * kKStride + 8 * (f & 15)) = r.k[j];
-  }
-  // V^T: row d = 8*dc + e holds keys 16*w + 4*kq .. +3 (register transpose of 4x8).
-#pragma unroll
-  for (int e2 = 0; e2 < 4; ++e2) {
-    const u32x2 lo = {pack_lo(r.v[0][e2], r.v[1][e2]), pack_lo(r.v[2][e2], r.v[3][e2])};
-    const u32x2 hi = {pack_hi(r.v[0][e2], r.v[1][e2]), pack_hi(r.v[2][e2], r.v[3][e2])};
-    *(u32x2*)(vts + (8 * dc + 2 * e2) * kVtStride + 16 * w + 4 * kq) = lo;
-    *(u32x2*)(vts + (8 * dc + 2 * e2 + 1) * kVtStride + 16 * w + 4 * kq) = hi;
+  for (int q = 0; q < kRowsPerWaveLoad / 4; ++q) {
+    const int row0 = kRowsPerWaveLoad * w + 4 * q;
+    const int row = row0 + (lane >> 4);
+    const int key = k0 + row;
+    const int chunk = (lane & 15) ^ (row & 15);
+    const bool ok = k0 >= 0 && key < p.seq_len;
+    const int ko = ok ? key * p.k_row_bytes + (chunk << 4) : kOutOfRange;
+    const int vo = ok ? key * p.v_row_bytes + (chunk << 4) : kOutOfRange;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (lds_void*)(stage + row0 * kRowBytes), 16, ko, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, (lds_void*)(stage + kTileBytes + row0 * kRowBytes), 16,
+                                             vo, 0, 0, 0);
   }
 }
+constexpr int kIssuePerTile = 2 * (kRowsPerWaveLoad / 4);  // DMA instructions per wave per tile
 
-// Copy the staged diagonal tile (keys k0..k0+63, one pool block) into the pool.
-__device__ __forceinline__ void write_pool(const Params& p, int b, int kvh, int k0, int tid,
-                                           int w, int dc, int kq, const TileRegs& r) {
+// Copy a resident tile (keys k0..k0+63, one pool block) from LDS into the pool.
+__device__ __forceinline__ void write_pool(const Params& p, const char* stage, int b, int kvh,
+                                           int k0, int tid) {
   const int lb = k0 / kKTile;
   if (lb >= p.max_blocks_per_seq) return;
   const int64_t phys = p.block_table[(int64_t)b * p.bt_stride + lb];
@@ -109,32 +112,120 @@ __device__ __forceinline__ void write_pool(const Params& p, int b, int kvh, int 
   const int64_t row_stride = (int64_t)p.num_kv_heads * kHeadDim;
   const int64_t base = phys * kKTile * row_stride + (int64_t)kvh * kHeadDim;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int f = 256 * j + tid;
+  for (int j = 0; j < kChunks; ++j) {
+    const int f = kThreads * j + tid;
     const int slot = f >> 4;
-    if (k0 + slot < p.seq_len)
-      *(u32x4*)(p.k_cache + base + slot * row_stride + 8 * (f & 15)) = r.k[j];
+    if (k0 + slot < p.seq_len) {
+      const u32x4 kv = *(const u32x4*)(stage + swz(slot, f & 15));
+      const u32x4 vv = *(const u32x4*)(stage + kTileBytes + swz(slot, f & 15));
+      *(u32x4*)(p.k_cache + base + slot * row_stride + 8 * (f & 15)) = kv;
+      *(u32x4*)(p.v_cache + base + slot * row_stride + 8 * (f & 15)) = vv;
+    }
   }
+}
+
+// V^T MFMA fragment half: lane (col = i, g) receives keys key0 + j (j = 0..3) of head_dim
+// column 16*dt + i, where key0 = row0 + 4g.  Lane i of each 16-lane group addresses row
+// row0 + 4g + i/4, columns 16*dt + 4*(i%4)..+3 (ds_read_b64_tr_b16 hands element i%4 of
+// lane 4j + i/4's 4-element chunk to lane i as element j).
+__device__ __forceinline__ u32x2 vt_read(const char* vs, int row0, int dt, int col, int g) {
+  typedef short s4 __attribute__((ext_vector_type(4)));
+  const int row = row0 + 4 * g + (col >> 2);
+  const int chunk = 2 * dt + ((col & 3) >> 1);
+  const char* ptr = vs + swz(row, chunk) + ((col & 1) << 3);
+  const s4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((s4 __attribute__((address_space(3)))*)ptr);
+  return __builtin_bit_cast(u32x2, v);
+}
+
+template <int HPW>
+__device__ __forceinline__ void consume_tile(const Params& p, const char* stage, int k0,
+                                             bool diag, int qpos, int col, int g,
+                                             const half8 (&qf)[HPW][4], float (&m_run)[HPW],
+                                             float (&l_run)[HPW], floatx4 (&acc)[HPW][8]) {
+  const char* ks = stage;
+  const char* vs = stage + kTileBytes;
+  const float c2 = p.scale_log2;  // > 0; the running max m is kept in raw score units
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int slot = 16 * w + 4 * kq + j;
-    if (k0 + slot < p.seq_len)
-      *(u32x4*)(p.v_cache + base + slot * row_stride + 8 * dc) = r.v[j];
+  for (int c = 0; c < 2; ++c) {  // two 32-key halves
+    // S^T = K Q^T: s[j][t] holds keys k0 + 32c + 16t + 4g + r for query column col.
+    floatx4 s[HPW][2];
+#pragma unroll
+    for (int j = 0; j < HPW; ++j) s[j][0] = s[j][1] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const half8 kf = as_half8(*(const u32x4*)(ks + swz(32 * c + 16 * t + col, 4 * i + g)));
+#pragma unroll
+        for (int j = 0; j < HPW; ++j) s[j][t] = mfma16x16x32(kf, qf[j][i], s[j][t]);
+      }
+    }
+    // online softmax per head: p = exp2(s*c2 - m*c2); l accumulates the fp16 p that the
+    // PV product uses (v_dot2_f32_f16 against ones); O is rescaled only when some row
+    // of the wave raised its maximum.
+    half8 pf[HPW];
+#pragma unroll
+    for (int j = 0; j < HPW; ++j) {
+      if (diag) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int key = k0 + 32 * c + 16 * t + 4 * g + r;
+            if (key > qpos || key >= p.seq_len) s[j][t][r] = -__builtin_inff();
+          }
+      }
+      float tmax = fmaxf(fmaxf(fmaxf(s[j][0][0], s[j][0][1]), fmaxf(s[j][0][2], s[j][0][3])),
+                         fmaxf(fmaxf(s[j][1][0], s[j][1][1]), fmaxf(s[j][1][2], s[j][1][3])));
+      tmax = row4_max(tmax);
+      const float m_old = m_run[j];
+      const float m_new = fmaxf(m_old, tmax);
+      m_run[j] = m_new;
+      const float mc = m_new * c2;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pf[j][4 * t + r] = (half_t)fast_exp2(__builtin_fmaf(s[j][t][r], c2, -mc));
+      typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+      const h2 one2 = {(half_t)1.f, (half_t)1.f};
+      float psum = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        psum = __builtin_amdgcn_fdot2(h2{pf[j][2 * e], pf[j][2 * e + 1]}, one2, psum, false);
+      if (__builtin_amdgcn_ballot_w64(m_new > m_old)) {
+        const float alpha = fast_exp2((m_old - m_new) * c2);
+        l_run[j] = l_run[j] * alpha + psum;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) acc[j][dt] *= alpha;
+      } else {
+        l_run[j] += psum;
+      }
+    }
+    // O^T += V^T P^T for these 32 keys: slots 0..3 = keys 4g..4g+3, 4..7 = 16+4g..16+4g+3
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const u32x2 a0 = vt_read(vs, 32 * c, dt, col, g);
+      const u32x2 a1 = vt_read(vs, 32 * c + 16, dt, col, g);
+      const half8 vf = as_half8(u32x4{a0[0], a0[1], a1[0], a1[1]});
+#pragma unroll
+      for (int j = 0; j < HPW; ++j) acc[j][dt] = mfma16x16x32(vf, pf[j], acc[j][dt]);
+    }
   }
 }
 
 template <int HPW>  // query heads per workgroup
-__global__ __launch_bounds__(256) void fwd_kernel(Params p) {
-  __shared__ __attribute__((aligned(16))) char smem_raw[kSmemBytes];
-  half_t* smem = (half_t*)smem_raw;
+__global__ __launch_bounds__(kThreads) void fwd_kernel(Params p) {
+  // three pipeline stages of one K tile + one V tile each (distinct objects, so the
+  // compiler tracks their DMA writes separately)
+  __shared__ __attribute__((aligned(16))) char st0[kStageBytes];
+  __shared__ __attribute__((aligned(16))) char st1[kStageBytes];
+  __shared__ __attribute__((aligned(16))) char st2[kStageBytes];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index (uniform)
   const int col = lane & 15;
   const int g = lane >> 4;
-  const int dc = lane >> 2;  // V loader: 8 head_dim values
-  const int kq = lane & 3;   // V loader: 4 consecutive keys
 
   const int qt = p.num_q_tiles - 1 - (int)blockIdx.y;  // heaviest tiles first
   const int q0 = qt * kQTile;
@@ -145,11 +236,13 @@ __global__ __launch_bounds__(256) void fwd_kernel(Params p) {
   const int hsub = hrem % p.hg_per_kv;
   const int head0 = kvh * p.group + hsub * HPW;
 
-  const half_t* kh = p.k + (int64_t)b * p.k_sb + (int64_t)kvh * p.k_sh;
-  const half_t* vh = p.v + (int64_t)b * p.v_sb + (int64_t)kvh * p.v_sh;
+  const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.k + (int64_t)b * p.k_sb + (int64_t)kvh * p.k_sh), (short)0, p.k_records, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.v + (int64_t)b * p.v_sb + (int64_t)kvh * p.v_sh), (short)0, p.v_records, kBufferWord3);
 
   // Q^T fragments: column col = query position q0 + 16w + col; MFMA i takes
-  // d = 32*i + 8*g + s in reduction slot 8*g + s (the K fragment uses the same map).
+  // d = 32*i + 8*g + s in reduction slot 8*g + s (K fragments use the same map).
   const int qpos = q0 + kRowsPerWave * w + col;
   half8 qf[HPW][4];
 #pragma unroll
@@ -160,7 +253,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(Params p) {
     for (int i = 0; i < 4; ++i) {
       u32x4 v = {0u, 0u, 0u, 0u};
       if (qpos < p.seq_len) v = *(const u32x4*)(qrow + 32 * i + 8 * g);
-      qf[j][i] = as_half8(v);
+      qf[j][i] = as_half8(v ^ p.q_sign);  // exact negation when sm_scale < 0
     }
   }
 
@@ -174,93 +267,50 @@ __global__ __launch_bounds__(256) void fwd_kernel(Params p) {
     for (int dt = 0; dt < 8; ++dt) acc[j][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
 
-  // Tile order: the diagonal tile (index qt) first, then tiles 0 .. qt-1.
-  const int n_tiles = qt + 1;
-  TileRegs regs;
-  load_tile(p, kh, vh, q0, tid, w, dc, kq, regs);
-  if (p.k_cache && hsub == 0) write_pool(p, b, kvh, q0, tid, w, dc, kq, regs);
-  store_tile(smem, tid, w, dc, kq, regs);
-  __syncthreads();
+  // Key tiles: the diagonal tiles (those holding this workgroup's own positions) first,
+  // then tiles 0, 1, ... before the diagonal.
+  const int total_kt = (p.seq_len + kKTile - 1) / kKTile;
+  const int kt_diag0 = q0 / kKTile;
+  const int n_diag = min(kQTile / kKTile, total_kt - kt_diag0);
+  const int n = kt_diag0 + n_diag;
+  auto key0 = [&](int idx) -> int {
+    if (idx >= n) return -1;  // past the end: loads read zeros
+    return (idx < n_diag ? kt_diag0 + idx : idx - n_diag) * kKTile;
+  };
+  const bool pool = p.k_cache != nullptr && hsub == 0;
+  const int wave_last = q0 + kRowsPerWave * w + kRowsPerWave - 1;  // last position of the wave
 
-  for (int idx = 0; idx < n_tiles; ++idx) {
-    const bool diag = idx == 0;
-    const int k0 = diag ? q0 : (idx - 1) * kKTile;
-    const bool more = idx + 1 < n_tiles;
-    if (more) load_tile(p, kh, vh, idx * kKTile, tid, w, dc, kq, regs);
-
-    const half_t* ks = smem + (idx & 1) * kStageHalfs;
-    const half_t* vts = ks + kKHalfs;
-
-    // ---- S^T = K Q^T: s[j][t] holds keys k0 + 16t + 4g + r for query column col.
-    floatx4 s[HPW][4];
-#pragma unroll
-    for (int j = 0; j < HPW; ++j)
-#pragma unroll
-      for (int t = 0; t < 4; ++t) s[j][t] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const half8 kf = as_half8(*(const u32x4*)(ks + (16 * t + col) * kKStride + 32 * i + 8 * g));
-#pragma unroll
-        for (int j = 0; j < HPW; ++j) s[j][t] = mfma16x16x32(kf, qf[j][i], s[j][t]);
-      }
-    }
-
-    // ---- online softmax per head (log2 domain).
-    half8 pf[HPW][2];
-#pragma unroll
-    for (int j = 0; j < HPW; ++j) {
-      float tmax = kNegBig;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float x = s[j][t][r] * p.scale_log2;
-          if (diag) {
-            const int key = k0 + 16 * t + 4 * g + r;
-            if (key > qpos || key >= p.seq_len) x = -__builtin_inff();
-          }
-          s[j][t][r] = x;
-          tmax = fmaxf(tmax, x);
-        }
-      }
-      tmax = row4_max(tmax);
-      const float m_new = fmaxf(m_run[j], tmax);
-      const float alpha = fast_exp2(m_run[j] - m_new);
-      m_run[j] = m_new;
-      float psum = 0.f;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float e = fast_exp2(s[j][t][r] - m_new);
-          psum += e;
-          pf[j][t >> 1][4 * (t & 1) + r] = (half_t)e;
-        }
-      }
-      l_run[j] = l_run[j] * alpha + psum;
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) acc[j][dt] *= alpha;
-    }
-
-    // ---- O^T += V^T P^T over the two 32-key chunks.
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const half_t* row = vts + (16 * dt + col) * kVtStride + 32 * c;
-        const u32x2 a0 = *(const u32x2*)(row + 4 * g);
-        const u32x2 a1 = *(const u32x2*)(row + 16 + 4 * g);
-        const half8 vf = as_half8(u32x4{a0[0], a0[1], a1[0], a1[1]});
-#pragma unroll
-        for (int j = 0; j < HPW; ++j) acc[j][dt] = mfma16x16x32(vf, pf[j][c], acc[j][dt]);
-      }
-    }
-
-    if (more) store_tile(smem + ((idx + 1) & 1) * kStageHalfs, tid, w, dc, kq, regs);
-    __syncthreads();
+  // Three-stage pipeline: while tile idx is consumed from one stage, tile idx+1 is
+  // resident or landing in the next and tile idx+2 is being fetched into the third.
+  // Each step ends with this wave's DMA for tile idx+1 complete, then a barrier.
+#define FI_PREFILL_STEP(IDX, CUR, NN)                                                   \
+  {                                                                                      \
+    const int i_ = (IDX);                                                                \
+    issue_tile(p, kr, vr, NN, key0(i_ + 2), w, lane);                                    \
+    const int k0 = key0(i_);                                                             \
+    const bool diag = i_ < n_diag;                                                       \
+    if (diag && pool) write_pool(p, CUR, b, kvh, k0, tid);                               \
+    if (!(diag && k0 > wave_last))                                                       \
+      consume_tile<HPW>(p, CUR, k0, diag, qpos, col, g, qf, m_run, l_run, acc);          \
+    if (diag && pool)                                                                    \
+      wait_vmcnt<0>();                                                                   \
+    else                                                                                 \
+      wait_vmcnt<kIssuePerTile>();                                                       \
+    __builtin_amdgcn_s_barrier();                                                        \
   }
+
+  issue_tile(p, kr, vr, st0, key0(0), w, lane);
+  issue_tile(p, kr, vr, st1, key0(1), w, lane);
+  wait_vmcnt<kIssuePerTile>();
+  __builtin_amdgcn_s_barrier();
+  for (int idx = 0; idx < n; idx += 3) {
+    FI_PREFILL_STEP(idx, st0, st2)
+    if (idx + 1 >= n) break;
+    FI_PREFILL_STEP(idx + 1, st1, st0)
+    if (idx + 2 >= n) break;
+    FI_PREFILL_STEP(idx + 2, st2, st1)
+  }
+#undef FI_PREFILL_STEP
 
   // ---- normalise and store: lane holds O[qpos][16*dt + 4*g + r].  The row sums
   // combine lanes of the same column, which share qpos, so the branch is uniform
@@ -278,7 +328,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(Params p) {
 }
 
 static int heads_per_wg(int64_t group) {
-  for (int h = 4; h >= 1; --h)
+  for (int h = 3; h >= 1; --h)
     if (group % h == 0) return h;
   return 1;
 }
@@ -357,7 +407,8 @@ extern "C" int fi_flash_attention_fwd(const void* q, const void* k, const void* 
   p.num_kv_heads = (int)num_kv_heads;
   p.group = (int)group;
   p.hg_per_kv = (int)(group / hpw);
-  p.scale_log2 = sm_scale * kLog2e;
+  p.scale_log2 = (sm_scale < 0 ? -sm_scale : sm_scale) * kLog2e;
+  p.q_sign = sm_scale < 0 ? 0x80008000u : 0u;
   p.num_q_tiles = (int)((seq_len + kQTile - 1) / kQTile);
   p.k_cache = (half_t*)k_cache;
   p.v_cache = (half_t*)v_cache;
@@ -365,6 +416,16 @@ extern "C" int fi_flash_attention_fwd(const void* q, const void* k, const void* 
   p.block_table = block_table;
   p.bt_stride = bt_stride;
   p.max_blocks_per_seq = (int)max_blocks_per_seq;
+  const int64_t k_span = (seq_len - 1) * k_ss * 2 + kHeadDim * 2;
+  const int64_t v_span = (seq_len - 1) * v_ss * 2 + kHeadDim * 2;
+  if (k_ss <= 0 || v_ss <= 0 || k_span >= kOutOfRange || v_span >= kOutOfRange) {
+    set_error("fi_flash_attention_fwd: one head's K/V rows must span < 2 GiB with positive strides");
+    return FI_ERR_UNSUPPORTED;
+  }
+  p.k_records = (int)k_span;
+  p.v_records = (int)v_span;
+  p.k_row_bytes = (int)(k_ss * 2);
+  p.v_row_bytes = (int)(v_ss * 2);
 
   const int64_t gx = batch * num_kv_heads * p.hg_per_kv;
   if (gx > 0x7fffffff || p.num_q_tiles > 65535) {
@@ -372,11 +433,8 @@ extern "C" int fi_flash_attention_fwd(const void* q, const void* k, const void* 
     return FI_ERR_UNSUPPORTED;
   }
   const dim3 grid((unsigned)gx, (unsigned)p.num_q_tiles);
-  const dim3 block(kWaves * 64);
+  const dim3 block(kThreads);
   switch (hpw) {
-    case 4:
-      hipLaunchKernelGGL(fwd_kernel<4>, grid, block, 0, (hipStream_t)stream, p);
-      break;
     case 3:
       hipLaunchKernelGGL(fwd_kernel<3>, grid, block, 0, (hipStream_t)stream, p);
       break;
