@@ -1,0 +1,367 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X attention hot path (paged decode + causal prefill).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Prints ONE JSON line.  Headline: paged decode at batch 32 (contexts uniform in
+[512, 4096], 24/8 heads, d 128, block 64, 2048-block pool, shuffled table) in GB/s of
+algorithmic HBM traffic; a "step" is one paged_attention call over the batch, with
+the K/V pools rotated over four copies (2 GiB) so the 256 MB last-level cache cannot
+serve them.  The same line carries:
+
+* ``prefill`` — causal prefill batch 4 x seq 4096 with the K/V pool write, TFLOP/s;
+* ``decode_b1_ctx256`` / ``prefill_b1_s512`` — the small configurations (latency);
+* ``decode_28layer_b64`` — a 28-layer decode step over per-layer pools, batch 64,
+  lognormal contexts (median 1024, sigma 0.5, clipped to [64, 4096]): step latency
+  and decode tokens/s;
+* ``roofline`` objects (achieved vs MI355X peak) and ``cpu_baseline`` objects: the C
+  restatement of the reference's kernels (oracle/ref_algo.c, OpenMP) timed on this
+  host's cores on a bounded sample, plus the eager torch fp32 oracle.
+
+Timing uses HIP events on torch's current stream, which is the stream every
+fast_infer_amd kernel is launched on.  Inputs are resident in HBM before timing.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "decode attn GB/s + prefill attn TFLOP/s (% of MI355X roofline), fp16"
+HQ, HKV, D, BS = 24, 8, 128, 64
+
+
+def _args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only", default="", help="comma list: decode,prefill,small,e2e")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a plain 1 GiB device copy (reference for PMC byte counters)")
+    return ap.parse_args()
+
+
+def _cores() -> int:
+    # the GPU box grants 16 host cores per GPU whatever the affinity mask shows
+    return max(1, min(16, len(os.sched_getaffinity(0))))
+
+
+class Timer:
+    """HIP events on the current stream around `steps` calls of fn."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def run(self, fn, steps: int, warmup: int) -> float:
+        torch = self.torch
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(steps):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / 1e3 / steps  # seconds per call
+
+
+def _table(torch, lens, pool_blocks, seed, width):
+    perm = torch.randperm(pool_blocks, generator=torch.Generator().manual_seed(seed)).int()
+    table = torch.full((len(lens), width), -1, dtype=torch.int32)
+    pos = 0
+    for b, n in enumerate(lens):
+        nb = math.ceil(n / BS)
+        table[b, :nb] = perm[pos:pos + nb]
+        pos += nb
+    assert pos <= pool_blocks
+    return table
+
+
+def bench_decode_b32(torch, fi, timer, steps, warmup, dev):
+    from fast_infer_amd import roofline as R
+
+    B, N = 32, 2048
+    lens = torch.randint(512, 4097, (B,), generator=torch.Generator().manual_seed(2)).tolist()
+    g = torch.Generator(device=dev).manual_seed(2)
+    pools = [(torch.randn(N, BS, HKV, D, device=dev, generator=g, dtype=torch.float16),
+              torch.randn(N, BS, HKV, D, device=dev, generator=g, dtype=torch.float16))
+             for _ in range(4)]
+    q = torch.randn(B, HQ, D, device=dev, generator=g, dtype=torch.float16)
+    table = _table(torch, lens, N, 2, 64).to(dev)
+    cl = torch.tensor(lens, dtype=torch.int32, device=dev)
+    ws = fi.paged_attention_workspace(B, HQ, HKV, 4096, D, dev)
+    it = [0]
+
+    def step():
+        kc, vc = pools[it[0] & 3]
+        it[0] += 1
+        fi.paged_attention(q, kc, vc, table, BS, 4096, context_lens=cl, workspace=ws)
+
+    t = timer.run(step, steps, warmup)
+    nbytes = R.decode_bytes(lens, HQ, HKV, D, BS)
+    gbs = nbytes / t / 1e9
+    return dict(t=t, bytes=nbytes, gbs=gbs, lens=lens, q=q, pools=pools[0], table=table)
+
+
+def bench_prefill(torch, fi, timer, steps, warmup, dev, B, S, pool_blocks, seed):
+    from fast_infer_amd import roofline as R
+
+    g = torch.Generator(device=dev).manual_seed(seed)
+    q = torch.randn(B, S, HQ, D, device=dev, generator=g, dtype=torch.float16).transpose(1, 2)
+    k = torch.randn(B, S, HKV, D, device=dev, generator=g, dtype=torch.float16).transpose(1, 2)
+    v = torch.randn(B, S, HKV, D, device=dev, generator=g, dtype=torch.float16).transpose(1, 2)
+    kc = torch.zeros(pool_blocks, BS, HKV, D, device=dev, dtype=torch.float16)
+    vc = torch.zeros_like(kc)
+    per_row = pool_blocks // B
+    table = torch.randperm(pool_blocks, generator=torch.Generator().manual_seed(seed)).int()
+    table = table.view(B, per_row).to(dev)
+
+    def step():
+        fi.flash_attention(q, k, v, k_cache=kc, v_cache=vc, block_table=table)
+
+    t = timer.run(step, steps, warmup)
+    flops = R.prefill_flops(B, HQ, S, D)
+    return dict(t=t, flops=flops, tflops=flops / t / 1e12, q=q, k=k, v=v,
+                scatter_bytes=R.prefill_scatter_bytes(B, S, HKV, D))
+
+
+def bench_decode_b1(torch, fi, timer, steps, warmup, dev):
+    from fast_infer_amd import roofline as R
+
+    g = torch.Generator(device=dev).manual_seed(0)
+    copies = 64  # 64 x 8 MiB pools rotate past the last-level cache
+    pools = [(torch.randn(64, BS, HKV, D, device=dev, generator=g, dtype=torch.float16),
+              torch.randn(64, BS, HKV, D, device=dev, generator=g, dtype=torch.float16))
+             for _ in range(copies)]
+    q = torch.randn(1, HQ, D, device=dev, generator=g, dtype=torch.float16)
+    table = torch.randperm(64, generator=torch.Generator().manual_seed(0)).int().view(1, 64).to(dev)
+    it = [0]
+
+    def step():
+        kc, vc = pools[it[0] % copies]
+        it[0] += 1
+        fi.paged_attention(q, kc, vc, table, BS, 256)
+
+    t = timer.run(step, steps, warmup)
+    nbytes = R.decode_bytes([256], HQ, HKV, D, BS)
+    return dict(t=t, bytes=nbytes, gbs=nbytes / t / 1e9)
+
+
+def bench_decode_28layer(torch, fi, timer, steps, warmup, dev):
+    from fast_infer_amd import roofline as R
+
+    L, B, N = 28, 64, 4096
+    gen = torch.Generator().manual_seed(4)
+    lens = torch.exp(torch.randn(B, generator=gen) * 0.5 + math.log(1024)).round()
+    lens = lens.clamp(64, 4096).int().tolist()
+    g = torch.Generator(device=dev).manual_seed(4)
+    kpool = torch.empty(L, N, BS, HKV, D, device=dev, dtype=torch.float16)
+    vpool = torch.empty_like(kpool)
+    for layer in range(L):
+        kpool[layer].normal_(generator=g)
+        vpool[layer].normal_(generator=g)
+    tables = [_table(torch, lens, N, 100 + layer, 64).to(dev) for layer in range(L)]
+    qs = torch.randn(L, B, HQ, D, device=dev, generator=g, dtype=torch.float16)
+    cl = torch.tensor(lens, dtype=torch.int32, device=dev)
+    ws = fi.paged_attention_workspace(B, HQ, HKV, 4096, D, dev)
+
+    def step():
+        for layer in range(L):
+            fi.paged_attention(qs[layer], kpool[layer], vpool[layer], tables[layer], BS, 4096,
+                               context_lens=cl, workspace=ws)
+
+    t = timer.run(step, max(1, steps // 10), max(1, warmup // 5))
+    nbytes = L * R.decode_bytes(lens, HQ, HKV, D, BS)
+    return dict(t=t, bytes=nbytes, gbs=nbytes / t / 1e9, tok_s=B / t, lens=lens)
+
+
+# ----------------------------------------------------------------------------- CPU
+
+
+def cpu_baseline_decode(torch, res, cores):
+    """C restatement (port) and torch fp32 oracle on the full batch-32 decode."""
+    import numpy as np
+
+    from oracle import attention as OA
+    from oracle import native
+
+    kc, vc = (t.cpu().numpy() for t in res["pools"])
+    q = res["q"].cpu().numpy()
+    table = res["table"].cpu().numpy()
+    lens = res["lens"]
+    native.load()
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        native.paged_forward(q, kc, vc, table, BS, lens, threads=cores)
+        reps += 1
+        if time.perf_counter() - t0 > 2.0:
+            break
+    t_port = (time.perf_counter() - t0) / reps
+    torch.set_num_threads(cores)
+    tq, tk, tv, tt = (torch.from_numpy(np.ascontiguousarray(a)) for a in (q, kc, vc, table))
+    t0 = time.perf_counter()
+    OA.paged_attention(tq, tk, tv, tt, BS, lens)
+    t_torch = time.perf_counter() - t0
+    return dict(port=res["bytes"] / t_port / 1e9, torch=res["bytes"] / t_torch / 1e9,
+                t_port=t_port, t_torch=t_torch, reps=reps)
+
+
+def cpu_baseline_prefill(torch, res, cores, B, S, nprog=16):
+    """C restatement on `nprog` of the B*24 (batch, head) programs, extrapolated;
+    torch fp32 oracle on 4 heads of batch row 0, extrapolated."""
+    from oracle import attention as OA
+    from oracle import native
+
+    q = res["q"].cpu().contiguous().numpy()
+    k = res["k"].cpu().contiguous().numpy()
+    v = res["v"].cpu().contiguous().numpy()
+    total = B * HQ
+    progs = [(i % B, (i * 7) % HQ) for i in range(nprog)]
+    native.load()
+    t0 = time.perf_counter()
+    native.flash_forward(q, k, v, programs=progs, threads=cores)
+    t_port = (time.perf_counter() - t0) * total / nprog
+    torch.set_num_threads(cores)
+    qt, kt, vt = (torch.from_numpy(a) for a in (q, k, v))
+    heads = [0, 5, 11, 23]
+    t0 = time.perf_counter()
+    for h in heads:
+        OA.causal_attention(qt[:1, h:h + 1], kt[:1, h // 3:h // 3 + 1], vt[:1, h // 3:h // 3 + 1])
+    t_torch = (time.perf_counter() - t0) * total / len(heads)
+    return dict(port=res["flops"] / t_port / 1e12, torch=res["flops"] / t_torch / 1e12,
+                t_port=t_port, t_torch=t_torch, nprog=nprog, total=total)
+
+
+def main():
+    a = _args()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {a.gpus} is not supported (the attention "
+              "path runs on a single MI355X here; see DESIGN.md for how it would shard).",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import fast_infer_amd as fi
+    from fast_infer_amd import roofline as R
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    timer = Timer(torch)
+    only = set(filter(None, a.only.split(","))) or {"decode", "prefill", "small", "e2e"}
+    cores = _cores()
+    steps, warm = a.steps, a.warmup
+    out = {"metric": METRIC}
+
+    if a.copy_calibration:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+
+    dec = None
+    if "decode" in only:
+        dec = bench_decode_b32(torch, fi, timer, steps, warm, dev)
+        print(f"[bench] decode b32: {dec['t'] * 1e6:.1f} us/call, {dec['gbs']:.0f} GB/s",
+              file=sys.stderr, flush=True)
+    pre = None
+    if "prefill" in only:
+        pre = bench_prefill(torch, fi, timer, max(1, steps // 5), max(1, warm // 2), dev,
+                            4, 4096, 256, 3)
+        print(f"[bench] prefill b4 s4096: {pre['t'] * 1e6:.1f} us/call, "
+              f"{pre['tflops']:.1f} TFLOP/s", file=sys.stderr, flush=True)
+
+    if dec is not None:
+        out.update({
+            "value": round(dec["gbs"], 1), "unit": "GB/s", "n_gpus": 1, "steps": steps,
+            "warmup": warm, "ms_per_step": round(dec["t"] * 1e3, 5),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+            "data": "synthetic: seeded N(0,1) fp16 q and K/V pools, seeded shuffled block tables",
+            "config": {"workload": "paged decode, batch 32, contexts U[512,4096], 24 q / 8 kv "
+                                   "heads, head_dim 128, block_size 64, 2048-block pool",
+                       "batch": 32, "context_tokens": sum(dec["lens"]),
+                       "num_q_heads": HQ, "num_kv_heads": HKV, "head_dim": D,
+                       "block_size": BS, "pool_blocks": 2048},
+            "roofline": {"bound": "hbm", "achieved": round(dec["gbs"], 1),
+                         "peak": R.HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(dec["gbs"] / R.HBM_PEAK_GBS, 4), "traffic": None,
+                         "kernel": "paged decode call (partition + merge launches)",
+                         "algorithmic_bytes": dec["bytes"]},
+        })
+    if pre is not None:
+        out["prefill"] = {
+            "workload": "causal prefill, batch 4, seq 4096, 24 q / 8 kv heads, head_dim 128, "
+                        "with the K/V write into a 256-block pool (block_size 64)",
+            "value": round(pre["tflops"], 2), "unit": "TFLOP/s",
+            "ms_per_step": round(pre["t"] * 1e3, 5), "steps": max(1, steps // 5),
+            "roofline": {"bound": "mfma", "achieved": round(pre["tflops"], 2),
+                         "peak": R.FP16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(pre["tflops"] / R.FP16_MFMA_PEAK_TFLOPS, 4),
+                         "traffic": None, "kernel": "fwd_kernel<3>",
+                         "algorithmic_flops": pre["flops"],
+                         "pool_write_bytes": pre["scatter_bytes"]},
+        }
+    if "small" in only:
+        d1 = bench_decode_b1(torch, fi, timer, steps, warm, dev)
+        p1 = bench_prefill(torch, fi, timer, steps, warm, dev, 1, 512, 64, 1)
+        out["decode_b1_ctx256"] = {"us_per_call": round(d1["t"] * 1e6, 2),
+                                   "GB/s": round(d1["gbs"], 1), "bytes": d1["bytes"]}
+        out["prefill_b1_s512"] = {"us_per_call": round(p1["t"] * 1e6, 2),
+                                  "TFLOP/s": round(p1["tflops"], 2)}
+        print(f"[bench] small: decode b1 {d1['t'] * 1e6:.1f} us, prefill s512 "
+              f"{p1['t'] * 1e6:.1f} us", file=sys.stderr, flush=True)
+    if "e2e" in only:
+        e = bench_decode_28layer(torch, fi, timer, steps, warm, dev)
+        out["decode_28layer_b64"] = {
+            "step_ms": round(e["t"] * 1e3, 4), "tokens_per_s": round(e["tok_s"], 1),
+            "GB/s": round(e["gbs"], 1), "frac_hbm": round(e["gbs"] / R.HBM_PEAK_GBS, 4),
+            "context_tokens": sum(e["lens"]), "lognormal_sigma": 0.5}
+        print(f"[bench] 28-layer b64 step: {e['t'] * 1e3:.3f} ms, {e['gbs']:.0f} GB/s",
+              file=sys.stderr, flush=True)
+
+    if not a.no_cpu_baseline:
+        if dec is not None:
+            c = cpu_baseline_decode(torch, dec, cores)
+            out["cpu_baseline"] = {
+                "value": round(c["port"], 3), "unit": "GB/s", "cores": cores, "kind": "port",
+                "sample": f"the full batch-32 decode call, C restatement of the reference "
+                          f"kernel (oracle/ref_algo.c, OpenMP), {c['reps']} reps, "
+                          f"{c['t_port'] * 1e3:.1f} ms/call",
+                "torch_fp32_oracle": {"value": round(c["torch"], 3), "unit": "GB/s",
+                                      "s_per_call": round(c["t_torch"], 3)}}
+            print(f"[bench] cpu decode: port {c['port']:.2f} GB/s, torch {c['torch']:.2f} GB/s",
+                  file=sys.stderr, flush=True)
+        if pre is not None:
+            c = cpu_baseline_prefill(torch, pre, cores, 4, 4096)
+            out["prefill"]["cpu_baseline"] = {
+                "value": round(c["port"], 4), "unit": "TFLOP/s", "cores": cores,
+                "kind": "port",
+                "sample": f"C restatement on {c['nprog']} of {c['total']} (batch, head) "
+                          f"programs, extrapolated to the full call "
+                          f"({c['t_port']:.1f} s/call)",
+                "torch_fp32_oracle": {"value": round(c["torch"], 4), "unit": "TFLOP/s",
+                                      "sample": "4 heads of batch row 0, extrapolated"}}
+            print(f"[bench] cpu prefill: port {c['port']:.4f} TFLOP/s", file=sys.stderr,
+                  flush=True)
+
+    out["device"] = torch.cuda.get_device_name(0)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -190,7 +190,11 @@ __device__ __forceinline__ void consume_iter(const Params& p, const IterRegs& r,
   wave_lds_sync();
 }
 
-__global__ __launch_bounds__(256, 2) void partition_kernel(Params p) {
+// kPipelined: two register buffers, the next iteration's loads in flight while the
+// current one is consumed (2 waves per SIMD).  Otherwise (the default) one buffer and
+// up to 4 waves per SIMD: more resident waves keep more loads in flight per CU.
+template <bool kPipelined>
+__global__ __launch_bounds__(256, kPipelined ? 2 : 3) void partition_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) char smem[kSmemBytes];
   __shared__ int s_tab[kMaxSplitEntries];
 
@@ -206,7 +210,15 @@ __global__ __launch_bounds__(256, 2) void partition_kernel(Params p) {
 
   const int ctx = row_context(p, b);
   const int split_start = split * p.tokens_per_split;
-  if (!p.direct && split_start >= ctx) return;  // no tokens here; the merge skips it
+  if (!p.direct && split_start >= ctx) {
+    // no tokens here: leave an empty partial (m = kNegBig, l = 0) for the merge
+    if (threadIdx.x < p.heads_per_wg) {
+      const int64_t slot = ((int64_t)b * p.num_q_heads + head0 + threadIdx.x) * p.max_splits + split;
+      p.part_ml[slot * 2 + 0] = kNegBig;
+      p.part_ml[slot * 2 + 1] = 0.f;
+    }
+    return;
+  }
   const int split_end = min(split_start + p.tokens_per_split, ctx);
 
   // Block-table entries of this partition, validated once, staged in LDS.
@@ -252,18 +264,27 @@ __global__ __launch_bounds__(256, 2) void partition_kernel(Params p) {
   // iteration it is consumed.  Loads past the partition read zeros (no traffic).
   const int first = split_start + w * kIterTokens;
   const int n_it = first < split_end ? (split_end - first + kWgTokens - 1) / kWgTokens : 0;
-  IterRegs ra, rb;
-  if (n_it > 0)
-    issue_iter(p, s_tab, tab0, first, split_end, kv_off, block_bytes, row_bytes, col, g, dc, kq, ra);
-  for (int it = 0; it < n_it; it += 2) {
-    const int b0 = first + it * kWgTokens;
-    issue_iter(p, s_tab, tab0, b0 + kWgTokens, split_end, kv_off, block_bytes, row_bytes, col, g,
-               dc, kq, rb);
-    consume_iter(p, ra, b0, split_end, qf, vt, col, g, dc, kq, m_run, l_run, acc);
-    if (it + 1 >= n_it) break;
-    issue_iter(p, s_tab, tab0, b0 + 2 * kWgTokens, split_end, kv_off, block_bytes, row_bytes, col,
-               g, dc, kq, ra);
-    consume_iter(p, rb, b0 + kWgTokens, split_end, qf, vt, col, g, dc, kq, m_run, l_run, acc);
+  if constexpr (kPipelined) {
+    IterRegs ra, rb;
+    if (n_it > 0)
+      issue_iter(p, s_tab, tab0, first, split_end, kv_off, block_bytes, row_bytes, col, g, dc, kq, ra);
+    for (int it = 0; it < n_it; it += 2) {
+      const int b0 = first + it * kWgTokens;
+      issue_iter(p, s_tab, tab0, b0 + kWgTokens, split_end, kv_off, block_bytes, row_bytes, col,
+                 g, dc, kq, rb);
+      consume_iter(p, ra, b0, split_end, qf, vt, col, g, dc, kq, m_run, l_run, acc);
+      if (it + 1 >= n_it) break;
+      issue_iter(p, s_tab, tab0, b0 + 2 * kWgTokens, split_end, kv_off, block_bytes, row_bytes,
+                 col, g, dc, kq, ra);
+      consume_iter(p, rb, b0 + kWgTokens, split_end, qf, vt, col, g, dc, kq, m_run, l_run, acc);
+    }
+  } else {
+    for (int it = 0; it < n_it; ++it) {
+      const int b0 = first + it * kWgTokens;
+      IterRegs ra;
+      issue_iter(p, s_tab, tab0, b0, split_end, kv_off, block_bytes, row_bytes, col, g, dc, kq, ra);
+      consume_iter(p, ra, b0, split_end, qf, vt, col, g, dc, kq, m_run, l_run, acc);
+    }
   }
 
   l_run = row4_sum(l_run);
@@ -314,37 +335,45 @@ __global__ __launch_bounds__(256, 2) void partition_kernel(Params p) {
 }
 
 // Merge the partition partials of one (row, query head): o = sum_s e^(m_s-M) o_s /
-// sum_s e^(m_s-M) l_s, zeros for an empty row.  The (m, l) pairs are staged in LDS
-// by all threads at once; the weighted sum over partitions then issues independent
-// loads per thread.
+// sum_s e^(m_s-M) l_s, zeros for an empty row.  Every partition of the row wrote a
+// partial (empty ones: m = kNegBig, l = 0), so all loads are issued at once with no
+// dependency on the row's length; empty partials are selected away, never multiplied.
 __global__ __launch_bounds__(kHeadDim) void merge_kernel(Params p) {
-  __shared__ float s_w[kMaxSplits];
-  __shared__ float s_l[kMaxSplits];
+  constexpr int kBatch = 8;
   const int h = blockIdx.x;
   const int b = blockIdx.y;
   const int d = threadIdx.x;
-  const int ctx = row_context(p, b);
-  const int nsplit = (ctx + p.tokens_per_split - 1) / p.tokens_per_split;
   const int64_t slot0 = ((int64_t)b * p.num_q_heads + h) * p.max_splits;
-  for (int s = d; s < nsplit; s += kHeadDim) {
-    s_w[s] = p.part_ml[(slot0 + s) * 2];
-    s_l[s] = p.part_ml[(slot0 + s) * 2 + 1];
+  float mx = kNegBig, L = 0.f, O = 0.f;
+  for (int s0 = 0; s0 < p.max_splits; s0 += kBatch) {
+    float m[kBatch], l[kBatch], o[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int s = s0 + k < p.max_splits ? s0 + k : p.max_splits - 1;
+      m[k] = p.part_ml[(slot0 + s) * 2];
+      l[k] = p.part_ml[(slot0 + s) * 2 + 1];
+      o[k] = p.part_o[(slot0 + s) * kHeadDim + d];
+    }
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const bool use = s0 + k < p.max_splits && l[k] > 0.f;
+      const float mk = use ? m[k] : kNegBig;
+      const float mn = fmaxf(mx, mk);
+      const float a = fast_exp2(mx - mn);
+      const float w = use ? fast_exp2(mk - mn) : 0.f;
+      L = L * a + w * l[k];
+      O = O * a + (use ? w * o[k] : 0.f);
+      mx = mn;
+    }
   }
-  __syncthreads();
-  float mx = kNegBig;
-  for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, s_w[s]);
-  float L = 0.f;
-  for (int s = 0; s < nsplit; ++s) L += fast_exp2(s_w[s] - mx) * s_l[s];
-  float O = 0.f;
-#pragma unroll 8
-  for (int s = 0; s < nsplit; ++s) O += fast_exp2(s_w[s] - mx) * p.part_o[(slot0 + s) * kHeadDim + d];
   p.o[(int64_t)b * p.o_sb + (int64_t)h * p.o_sh + d] = (half_t)(L > 0.f ? O / L : 0.f);
 }
 
-// Partition size (tokens, a multiple of kWgTokens, at most kMaxSplitTokens) for a call.
-// Aims for about kTargetWgs workgroups so the 256 CUs stay busy at small batch; a
-// context that fits in four workgroup iterations is served by one partition and no
-// merge.  FI_DECODE_TOKENS_PER_SPLIT overrides the choice (for tuning sweeps).
+// Partition size (tokens, a multiple of kWgTokens) for a call: about kTargetWgs
+// workgroups in total, 128..256 tokens each (short partitions keep every CU streaming
+// at small batch and balance ragged rows; the merge reads ~0.5 KiB per partition and
+// head).  A context that fits in four workgroup iterations is one partition with no
+// merge.  FI_DECODE_TOKENS_PER_SPLIT / FI_DECODE_TARGET_WGS override (tuning sweeps).
 static int tokens_per_split(int64_t batch, int64_t wg_per_row, int64_t num_tokens) {
   static int env_tps = -1;
   if (env_tps < 0) {
@@ -358,7 +387,7 @@ static int tokens_per_split(int64_t batch, int64_t wg_per_row, int64_t num_token
     env_target = s ? atoi(s) : 0;
     if (env_target < 0) env_target = 0;
   }
-  const int64_t target = env_target > 0 ? env_target : 2048;
+  const int64_t target = env_target > 0 ? env_target : 4096;
   int64_t tps;
   if (env_tps > 0) {
     tps = env_tps;
@@ -369,6 +398,7 @@ static int tokens_per_split(int64_t batch, int64_t wg_per_row, int64_t num_token
     int64_t want = (target + per_row - 1) / per_row;
     if (want < 1) want = 1;
     tps = (num_tokens + want - 1) / want;
+    if (tps > 2 * kWgTokens) tps = 2 * kWgTokens;
   }
   const int64_t min_tps = (num_tokens + kMaxSplits - 1) / kMaxSplits;
   if (tps < min_tps) tps = min_tps;
@@ -493,8 +523,16 @@ extern "C" int fi_paged_attention_fwd(const void* q, int64_t q_sb, int64_t q_sh,
     set_error("fi_paged_attention_fwd: grid too large");
     return FI_ERR_UNSUPPORTED;
   }
-  hipLaunchKernelGGL(partition_kernel, dim3((unsigned)wg_per_row, (unsigned)splits, (unsigned)batch),
-                     dim3(kWaves * 64), 0, (hipStream_t)stream, p);
+  static int variant = -1;  // FI_DECODE_VARIANT=1: the 2-deep pipelined kernel (tuning)
+  if (variant < 0) {
+    const char* s = getenv("FI_DECODE_VARIANT");
+    variant = s ? atoi(s) : 0;
+  }
+  const dim3 grid((unsigned)wg_per_row, (unsigned)splits, (unsigned)batch);
+  if (variant == 1)
+    hipLaunchKernelGGL(partition_kernel<true>, grid, dim3(kWaves * 64), 0, (hipStream_t)stream, p);
+  else
+    hipLaunchKernelGGL(partition_kernel<false>, grid, dim3(kWaves * 64), 0, (hipStream_t)stream, p);
   int rc = check_launch("fi_paged_attention_fwd(partition)");
   if (rc != FI_OK || p.direct) return rc;
   hipLaunchKernelGGL(merge_kernel, dim3((unsigned)num_q_heads, (unsigned)batch), dim3(kHeadDim), 0,
