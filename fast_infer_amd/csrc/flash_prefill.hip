@@ -34,6 +34,7 @@ constexpr int kRowsPerWaveLoad = kKTile / kWaves;  // K (and V) tile rows each w
 constexpr int kChunks = kKTile * 16 / kThreads;     // 16-byte chunks of K (and V) per thread
 constexpr int kOutOfRange = 0x7ffffff0;          // buffer offset past any tensor: loads give 0
 constexpr int kBufferWord3 = 0x00020000;
+constexpr float kLazyLog2 = 8.f;  // the reference max may lag the true max by 2^8
 static_assert(kQTile % kKTile == 0, "query tiles cover whole key tiles");
 
 struct Params {
@@ -50,6 +51,7 @@ struct Params {
   int group;         // query heads per kv head
   int hg_per_kv;     // workgroups per kv head (group / heads per workgroup)
   float scale_log2;  // |sm_scale| * log2(e)
+  float lazy_raw;    // kLazyLog2 / scale_log2: slack of the reference max in raw units
   uint32_t q_sign;   // 0x80008000 when sm_scale < 0: Q is negated instead of the scale
   int num_q_tiles;
   int k_records;     // bytes addressable from one (batch, kv head) base of k
@@ -65,9 +67,13 @@ struct Params {
 };
 
 // Byte address in a K or V LDS tile of 16-byte chunk c (0..15) of row r: rows are
-// 256 bytes, chunks XOR-swizzled by the row so that 16 consecutive rows read at one
-// column hit 16 different bank groups.
-__device__ __forceinline__ int swz(int r, int c) { return r * kRowBytes + ((c ^ (r & 15)) << 4); }
+// 256 bytes, chunks XOR-swizzled by f(r) = ((r & 7) << 1) | ((r >> 3) & 1), a bijection
+// on r & 15.  16 consecutive rows read at one column (K fragments) hit 16 different
+// chunk slots, and the 32-byte pair a transposed V read takes from each of 8
+// consecutive rows lands in 8 different pair slots (f's pair index is r & 7).
+__device__ __forceinline__ int swz(int r, int c) {
+  return r * kRowBytes + ((c ^ (((r & 7) << 1) | ((r >> 3) & 1))) << 4);
+}
 
 // Wait until at most `n` of this wave's vector-memory operations are outstanding
 // (vmcnt only; LDS and export counters untouched).
@@ -80,7 +86,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 // Issue the direct-to-LDS loads of this wave's rows of the K/V tile at key k0 into
 // `stage` (K at +0, V at +kTileBytes).  One instruction moves 4 rows (64 lanes x 16
 // bytes) to 1 KiB of consecutive LDS; lane l fills swizzled position l%16 of row
-// 4q + l/16, so it fetches global chunk (l%16) ^ (row & 15).  Rows past seq_len, or a
+// 4q + l/16, so it fetches global chunk (l%16) ^ f(row) (see swz).  Rows past seq_len, or a
 // tile past the end (k0 < 0), fetch zeros through the buffer bounds check.
 __device__ __forceinline__ void issue_tile(const Params& p, __amdgpu_buffer_rsrc_t kr,
                                            __amdgpu_buffer_rsrc_t vr, char* stage, int k0,
@@ -91,7 +97,7 @@ __device__ __forceinline__ void issue_tile(const Params& p, __amdgpu_buffer_rsrc
     const int row0 = kRowsPerWaveLoad * w + 4 * q;
     const int row = row0 + (lane >> 4);
     const int key = k0 + row;
-    const int chunk = (lane & 15) ^ (row & 15);
+    const int chunk = (lane & 15) ^ (((row & 7) << 1) | ((row >> 3) & 1));
     const bool ok = k0 >= 0 && key < p.seq_len;
     const int ko = ok ? key * p.k_row_bytes + (chunk << 4) : kOutOfRange;
     const int vo = ok ? key * p.v_row_bytes + (chunk << 4) : kOutOfRange;
@@ -160,9 +166,12 @@ __device__ __forceinline__ void consume_tile(const Params& p, const char* stage,
         for (int j = 0; j < HPW; ++j) s[j][t] = mfma16x16x32(kf, qf[j][i], s[j][t]);
       }
     }
-    // online softmax per head: p = exp2(s*c2 - m*c2); l accumulates the fp16 p that the
-    // PV product uses (v_dot2_f32_f16 against ones); O is rescaled only when some row
-    // of the wave raised its maximum.
+    // Online softmax per head with a lazily moved reference max m (raw score units):
+    // p = exp2(s*c2 - m*c2).  m only moves when some score exceeds it by more than
+    // kLazyLog2 in the log2 domain, so p <= 2^kLazyLog2 (exact in fp16, O and l in fp32)
+    // and the softmax is unchanged; the test needs no cross-lane step, and the row max
+    // is reduced across the column's four lanes only when m moves.  l accumulates the
+    // fp16 p that the PV product uses (v_dot2_f32_f16 against ones).
     half8 pf[HPW];
 #pragma unroll
     for (int j = 0; j < HPW; ++j) {
@@ -175,31 +184,30 @@ __device__ __forceinline__ void consume_tile(const Params& p, const char* stage,
             if (key > qpos || key >= p.seq_len) s[j][t][r] = -__builtin_inff();
           }
       }
-      float tmax = fmaxf(fmaxf(fmaxf(s[j][0][0], s[j][0][1]), fmaxf(s[j][0][2], s[j][0][3])),
-                         fmaxf(fmaxf(s[j][1][0], s[j][1][1]), fmaxf(s[j][1][2], s[j][1][3])));
-      tmax = row4_max(tmax);
-      const float m_old = m_run[j];
-      const float m_new = fmaxf(m_old, tmax);
-      m_run[j] = m_new;
-      const float mc = m_new * c2;
+      float lmax = fmaxf(fmaxf(fmaxf(s[j][0][0], s[j][0][1]), s[j][0][2]), s[j][0][3]);
+      lmax = fmaxf(fmaxf(fmaxf(fmaxf(lmax, s[j][1][0]), s[j][1][1]), s[j][1][2]), s[j][1][3]);
+      if (__builtin_amdgcn_ballot_w64(lmax > m_run[j] + p.lazy_raw)) {
+        const float m_old = m_run[j];
+        const float rmax = row4_max(lmax);
+        const float m_new = rmax > m_old + p.lazy_raw ? rmax : m_old;
+        const float alpha = fast_exp2((m_old - m_new) * c2);
+        m_run[j] = m_new;
+        l_run[j] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) acc[j][dt] *= alpha;
+      }
+      const float mc = m_run[j] * c2;
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int r = 0; r < 4; ++r) pf[j][4 * t + r] = (half_t)fast_exp2(__builtin_fmaf(s[j][t][r], c2, -mc));
       typedef _Float16 h2 __attribute__((ext_vector_type(2)));
       const h2 one2 = {(half_t)1.f, (half_t)1.f};
-      float psum = 0.f;
+      float psum = l_run[j];
 #pragma unroll
       for (int e = 0; e < 4; ++e)
         psum = __builtin_amdgcn_fdot2(h2{pf[j][2 * e], pf[j][2 * e + 1]}, one2, psum, false);
-      if (__builtin_amdgcn_ballot_w64(m_new > m_old)) {
-        const float alpha = fast_exp2((m_old - m_new) * c2);
-        l_run[j] = l_run[j] * alpha + psum;
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) acc[j][dt] *= alpha;
-      } else {
-        l_run[j] += psum;
-      }
+      l_run[j] = psum;
     }
     // O^T += V^T P^T for these 32 keys: slots 0..3 = keys 4g..4g+3, 4..7 = 16+4g..16+4g+3
 #pragma unroll
@@ -409,6 +417,7 @@ extern "C" int fi_flash_attention_fwd(const void* q, const void* k, const void* 
   p.hg_per_kv = (int)(group / hpw);
   p.scale_log2 = (sm_scale < 0 ? -sm_scale : sm_scale) * kLog2e;
   p.q_sign = sm_scale < 0 ? 0x80008000u : 0u;
+  p.lazy_raw = p.scale_log2 > 0.f ? kLazyLog2 / p.scale_log2 : 0.f;
   p.num_q_tiles = (int)((seq_len + kQTile - 1) / kQTile);
   p.k_cache = (half_t*)k_cache;
   p.v_cache = (half_t*)v_cache;
