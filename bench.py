@@ -14,7 +14,8 @@ serve them.  The same line carries:
 * ``decode_28layer_b64`` — a 28-layer decode step over per-layer pools, batch 64,
   lognormal contexts (median 1024, sigma 0.5, clipped to [64, 4096]): step latency
   and decode tokens/s;
-* ``roofline`` objects (achieved vs MI355X peak) and ``cpu_baseline`` objects: the C
+* ``roofline`` objects (achieved vs MI355X peak; ``traffic`` = HBM bytes per call measured by
+  rocprofv3 FETCH_SIZE/WRITE_SIZE, profiles/hbm_traffic.txt) and ``cpu_baseline`` objects: the C
   restatement of the reference's kernels (oracle/ref_algo.c, OpenMP) timed on this
   host's cores on a bounded sample, plus the eager torch fp32 oracle.
 
@@ -49,6 +50,19 @@ def _args():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device copy (reference for PMC byte counters)")
     return ap.parse_args()
+
+
+def _traffic(workload: str):
+    """HBM bytes per call (read + write) measured by rocprofv3 for this workload, from
+    profiles/hbm_traffic.txt; None when not measured."""
+    path = ROOT / "profiles" / "hbm_traffic.txt"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        parts = line.split()
+        if len(parts) == 3 and parts[0] == workload and not line.startswith("#"):
+            return int(parts[1]) + int(parts[2])
+    return None
 
 
 def _cores() -> int:
@@ -299,7 +313,8 @@ def main():
                        "block_size": BS, "pool_blocks": 2048},
             "roofline": {"bound": "hbm", "achieved": round(dec["gbs"], 1),
                          "peak": R.HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(dec["gbs"] / R.HBM_PEAK_GBS, 4), "traffic": None,
+                         "frac": round(dec["gbs"] / R.HBM_PEAK_GBS, 4),
+                         "traffic": _traffic("decode_b32"),
                          "kernel": "paged decode call (partition + merge launches)",
                          "algorithmic_bytes": dec["bytes"]},
         })
@@ -312,7 +327,7 @@ def main():
             "roofline": {"bound": "mfma", "achieved": round(pre["tflops"], 2),
                          "peak": R.FP16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(pre["tflops"] / R.FP16_MFMA_PEAK_TFLOPS, 4),
-                         "traffic": None, "kernel": "fwd_kernel<3>",
+                         "traffic": _traffic("prefill_b4_s4096"), "kernel": "fwd_kernel<3>",
                          "algorithmic_flops": pre["flops"],
                          "pool_write_bytes": pre["scatter_bytes"]},
         }

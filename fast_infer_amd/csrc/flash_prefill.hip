@@ -35,6 +35,7 @@ constexpr int kChunks = kKTile * 16 / kThreads;     // 16-byte chunks of K (and 
 constexpr int kOutOfRange = 0x7ffffff0;          // buffer offset past any tensor: loads give 0
 constexpr int kBufferWord3 = 0x00020000;
 constexpr float kLazyLog2 = 8.f;  // the reference max may lag the true max by 2^8
+
 static_assert(kQTile % kKTile == 0, "query tiles cover whole key tiles");
 
 struct Params {
