@@ -3,33 +3,34 @@
 // Replaces _flash_attn_fwd (kernels/attention.py:8-77) and its launcher (:80-113).
 // Same result — softmax(Q K^T * sm_scale, causal) V per query head, fp32 online
 // softmax, fp16 output — but laid out for MI355X:
-//   * a workgroup owns 64 query positions of all query heads that share one kv head
-//     (up to 4), so a K/V tile staged in LDS feeds every head of the GQA group and K/V
+//   * a workgroup (8 waves) owns 128 query positions of up to 3 query heads that share
+//     one kv head, so a K/V tile staged in LDS feeds every head of the GQA group and K/V
 //     are never expanded (the reference call site expands them, model.py:110-111);
 //   * the grid covers (query tile, head group, batch) with the heaviest causal tiles
 //     dispatched first, instead of one program walking a whole head (:34);
 //   * S^T = K Q^T and O^T = V^T P^T run on v_mfma_f32_16x16x32_f16: the lane holding a
 //     query column keeps its scores, P and O in registers with no shuffles between the
-//     two products; K tiles are read from LDS as A fragments, V is transposed once per
-//     tile while being staged into LDS (V^T rows);
-//   * K/V tiles are double-buffered in LDS with the next tile's global loads in flight
-//     during the current tile's MFMAs;
+//     two products; K fragments are read from LDS as A operands and V^T fragments with
+//     the LDS transpose read (ds_read_b64_tr_b16);
+//   * 128-key K/V tiles are copied global->LDS by the buffer unit (no register staging),
+//     double-buffered so the next tile's copy is in flight during the current tile;
 //   * the diagonal tile is processed first; when a pool is given, the workgroup that
-//     owns a 64-token block of K/V also copies it into the paged pool (the write of
-//     model.py:176-183), so the scatter costs no extra read.
+//     owns a tile of K/V also copies its two 64-token blocks into the paged pool (the
+//     write of model.py:176-183), so the scatter costs no extra read.
 #include "common.h"
 
 namespace fi {
 namespace prefill {
 
-constexpr int kWaves = 8;
+constexpr int kWaves = 8;                        // two waves per SIMD
 constexpr int kThreads = kWaves * 64;
 constexpr int kRowsPerWave = 16;                 // query positions per wave
 constexpr int kQTile = kWaves * kRowsPerWave;    // query positions per workgroup (128)
-constexpr int kKTile = 64;                       // keys per K/V tile (one pool block)
+constexpr int kKTile = 128;                      // keys per K/V tile (two pool blocks)
+constexpr int kPoolBlock = 64;                   // block_size of the fused pool write
 constexpr int kRowBytes = kHeadDim * 2;          // one K or V row in LDS (256 bytes)
 constexpr int kTileBytes = kKTile * kRowBytes;   // 16 KiB
-constexpr int kStageBytes = 2 * kTileBytes;      // K tile + V tile
+constexpr int kStageBytes = 2 * kTileBytes;      // K tile + V tile (2 stages: 128 KiB)
 constexpr int kRowsPerWaveLoad = kKTile / kWaves;  // K (and V) tile rows each wave loads
 constexpr int kChunks = kKTile * 16 / kThreads;     // 16-byte chunks of K (and V) per thread
 constexpr int kOutOfRange = 0x7ffffff0;          // buffer offset past any tensor: loads give 0
@@ -37,6 +38,7 @@ constexpr int kBufferWord3 = 0x00020000;
 constexpr float kLazyLog2 = 8.f;  // the reference max may lag the true max by 2^8
 
 static_assert(kQTile % kKTile == 0, "query tiles cover whole key tiles");
+static_assert(kKTile % kPoolBlock == 0, "a key tile covers whole pool blocks");
 
 struct Params {
   const half_t* q;
@@ -89,13 +91,15 @@ __device__ __forceinline__ void wait_vmcnt() {
 // bytes) to 1 KiB of consecutive LDS; lane l fills swizzled position l%16 of row
 // 4q + l/16, so it fetches global chunk (l%16) ^ f(row) (see swz).  Rows past seq_len, or a
 // tile past the end (k0 < 0), fetch zeros through the buffer bounds check.
+template <int NW = kWaves>
 __device__ __forceinline__ void issue_tile(const Params& p, __amdgpu_buffer_rsrc_t kr,
                                            __amdgpu_buffer_rsrc_t vr, char* stage, int k0,
                                            int w, int lane) {
   typedef void __attribute__((address_space(3))) lds_void;
+  constexpr int kRows = kKTile / NW;  // K (and V) rows this wave loads
 #pragma unroll
-  for (int q = 0; q < kRowsPerWaveLoad / 4; ++q) {
-    const int row0 = kRowsPerWaveLoad * w + 4 * q;
+  for (int q = 0; q < kRows / 4; ++q) {
+    const int row0 = kRows * w + 4 * q;
     const int row = row0 + (lane >> 4);
     const int key = k0 + row;
     const int chunk = (lane & 15) ^ (((row & 7) << 1) | ((row >> 3) & 1));
@@ -109,25 +113,26 @@ __device__ __forceinline__ void issue_tile(const Params& p, __amdgpu_buffer_rsrc
 }
 constexpr int kIssuePerTile = 2 * (kRowsPerWaveLoad / 4);  // DMA instructions per wave per tile
 
-// Copy a resident tile (keys k0..k0+63, one pool block) from LDS into the pool.
+// Copy a resident tile (keys k0..k0+kKTile-1, whole pool blocks of 64) from LDS into
+// the pool.
+template <int NT = kThreads>
 __device__ __forceinline__ void write_pool(const Params& p, const char* stage, int b, int kvh,
                                            int k0, int tid) {
-  const int lb = k0 / kKTile;
-  if (lb >= p.max_blocks_per_seq) return;
-  const int64_t phys = p.block_table[(int64_t)b * p.bt_stride + lb];
-  if (phys < 0 || phys >= p.num_pool_blocks) return;
   const int64_t row_stride = (int64_t)p.num_kv_heads * kHeadDim;
-  const int64_t base = phys * kKTile * row_stride + (int64_t)kvh * kHeadDim;
 #pragma unroll
-  for (int j = 0; j < kChunks; ++j) {
-    const int f = kThreads * j + tid;
-    const int slot = f >> 4;
-    if (k0 + slot < p.seq_len) {
-      const u32x4 kv = *(const u32x4*)(stage + swz(slot, f & 15));
-      const u32x4 vv = *(const u32x4*)(stage + kTileBytes + swz(slot, f & 15));
-      *(u32x4*)(p.k_cache + base + slot * row_stride + 8 * (f & 15)) = kv;
-      *(u32x4*)(p.v_cache + base + slot * row_stride + 8 * (f & 15)) = vv;
-    }
+  for (int j = 0; j < kKTile * 16 / NT; ++j) {
+    const int f = NT * j + tid;
+    const int slot = f >> 4;  // row within the tile
+    const int key = k0 + slot;
+    if (key >= p.seq_len) continue;
+    const int lb = key / kPoolBlock;
+    if (lb >= p.max_blocks_per_seq) continue;
+    const int64_t phys = p.block_table[(int64_t)b * p.bt_stride + lb];
+    if (phys < 0 || phys >= p.num_pool_blocks) continue;
+    const int64_t dst = (phys * kPoolBlock + key % kPoolBlock) * row_stride +
+                        (int64_t)kvh * kHeadDim + 8 * (f & 15);
+    *(u32x4*)(p.k_cache + dst) = *(const u32x4*)(stage + swz(slot, f & 15));
+    *(u32x4*)(p.v_cache + dst) = *(const u32x4*)(stage + kTileBytes + swz(slot, f & 15));
   }
 }
 
@@ -144,16 +149,34 @@ __device__ __forceinline__ u32x2 vt_read(const char* vs, int row0, int dt, int c
   return __builtin_bit_cast(u32x2, v);
 }
 
+// PV of half c of a resident tile: O^T += V^T P^T (slots 0..3 = keys 4g..4g+3,
+// 4..7 = 16+4g..16+4g+3).
+template <int HPW>
+__device__ __forceinline__ void pv_half8(const char* vs, int c, int col, int g,
+                                         const half8 (&pf)[HPW], floatx4 (&acc)[HPW][8]) {
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) {
+    const u32x2 a0 = vt_read(vs, 32 * c, dt, col, g);
+    const u32x2 a1 = vt_read(vs, 32 * c + 16, dt, col, g);
+    const half8 vf = as_half8(u32x4{a0[0], a0[1], a1[0], a1[1]});
+#pragma unroll
+    for (int j = 0; j < HPW; ++j) acc[j][dt] = mfma16x16x32(vf, pf[j], acc[j][dt]);
+  }
+}
+
+// One key tile: for each 32-key half, S^T = K Q^T, the online softmax, and PV.
 template <int HPW>
 __device__ __forceinline__ void consume_tile(const Params& p, const char* stage, int k0,
-                                             bool diag, int qpos, int col, int g,
-                                             const half8 (&qf)[HPW][4], float (&m_run)[HPW],
-                                             float (&l_run)[HPW], floatx4 (&acc)[HPW][8]) {
+                                             bool diag, int qpos, int wave_last, int col,
+                                             int g, const half8 (&qf)[HPW][4],
+                                             float (&m_run)[HPW], float (&l_run)[HPW],
+                                             floatx4 (&acc)[HPW][8]) {
   const char* ks = stage;
   const char* vs = stage + kTileBytes;
   const float c2 = p.scale_log2;  // > 0; the running max m is kept in raw score units
 #pragma unroll
-  for (int c = 0; c < 2; ++c) {  // two 32-key halves
+  for (int c = 0; c < kKTile / 32; ++c) {  // 32-key slices
+    if (diag && k0 + 32 * c > wave_last) break;  // slices wholly above this wave's diagonal
     // S^T = K Q^T: s[j][t] holds keys k0 + 32c + 16t + 4g + r for query column col.
     floatx4 s[HPW][2];
 #pragma unroll
@@ -210,25 +233,16 @@ __device__ __forceinline__ void consume_tile(const Params& p, const char* stage,
         psum = __builtin_amdgcn_fdot2(h2{pf[j][2 * e], pf[j][2 * e + 1]}, one2, psum, false);
       l_run[j] = psum;
     }
-    // O^T += V^T P^T for these 32 keys: slots 0..3 = keys 4g..4g+3, 4..7 = 16+4g..16+4g+3
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const u32x2 a0 = vt_read(vs, 32 * c, dt, col, g);
-      const u32x2 a1 = vt_read(vs, 32 * c + 16, dt, col, g);
-      const half8 vf = as_half8(u32x4{a0[0], a0[1], a1[0], a1[1]});
-#pragma unroll
-      for (int j = 0; j < HPW; ++j) acc[j][dt] = mfma16x16x32(vf, pf[j], acc[j][dt]);
-    }
+    pv_half8<HPW>(vs, c, col, g, pf, acc);
   }
 }
 
 template <int HPW>  // query heads per workgroup
 __global__ __launch_bounds__(kThreads) void fwd_kernel(Params p) {
-  // three pipeline stages of one K tile + one V tile each (distinct objects, so the
+  // two pipeline stages of one K tile + one V tile each (distinct objects, so the
   // compiler tracks their DMA writes separately)
   __shared__ __attribute__((aligned(16))) char st0[kStageBytes];
   __shared__ __attribute__((aligned(16))) char st1[kStageBytes];
-  __shared__ __attribute__((aligned(16))) char st2[kStageBytes];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -289,35 +303,28 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(Params p) {
   const bool pool = p.k_cache != nullptr && hsub == 0;
   const int wave_last = q0 + kRowsPerWave * w + kRowsPerWave - 1;  // last position of the wave
 
-  // Three-stage pipeline: while tile idx is consumed from one stage, tile idx+1 is
-  // resident or landing in the next and tile idx+2 is being fetched into the third.
-  // Each step ends with this wave's DMA for tile idx+1 complete, then a barrier.
-#define FI_PREFILL_STEP(IDX, CUR, NN)                                                   \
+  // Two-stage pipeline over 128-key tiles (tile idx in stage idx % 2): issue the DMA of
+  // tile idx+1 into the other stage (its last reader finished before the previous
+  // barrier), consume tile idx, wait for this wave's DMA of tile idx+1, barrier.
+#define FI_PREFILL_STEP(IDX, CUR, NXT)                                                   \
   {                                                                                      \
     const int i_ = (IDX);                                                                \
-    issue_tile(p, kr, vr, NN, key0(i_ + 2), w, lane);                                    \
+    issue_tile(p, kr, vr, NXT, key0(i_ + 1), w, lane);                                   \
     const int k0 = key0(i_);                                                             \
     const bool diag = i_ < n_diag;                                                       \
     if (diag && pool) write_pool(p, CUR, b, kvh, k0, tid);                               \
-    if (!(diag && k0 > wave_last))                                                       \
-      consume_tile<HPW>(p, CUR, k0, diag, qpos, col, g, qf, m_run, l_run, acc);          \
-    if (diag && pool)                                                                    \
-      wait_vmcnt<0>();                                                                   \
-    else                                                                                 \
-      wait_vmcnt<kIssuePerTile>();                                                       \
+    consume_tile<HPW>(p, CUR, k0, diag, qpos, wave_last, col, g, qf, m_run, l_run, acc); \
+    wait_vmcnt<0>();                                                                     \
     __builtin_amdgcn_s_barrier();                                                        \
   }
 
   issue_tile(p, kr, vr, st0, key0(0), w, lane);
-  issue_tile(p, kr, vr, st1, key0(1), w, lane);
-  wait_vmcnt<kIssuePerTile>();
+  wait_vmcnt<0>();
   __builtin_amdgcn_s_barrier();
-  for (int idx = 0; idx < n; idx += 3) {
-    FI_PREFILL_STEP(idx, st0, st2)
+  for (int idx = 0; idx < n; idx += 2) {
+    FI_PREFILL_STEP(idx, st0, st1)
     if (idx + 1 >= n) break;
     FI_PREFILL_STEP(idx + 1, st1, st0)
-    if (idx + 2 >= n) break;
-    FI_PREFILL_STEP(idx + 2, st2, st1)
   }
 #undef FI_PREFILL_STEP
 
@@ -390,9 +397,9 @@ extern "C" int fi_flash_attention_fwd(const void* q, const void* k, const void* 
       set_error("fi_flash_attention_fwd: pool write needs v_cache and block_table");
       return FI_ERR_INVALID;
     }
-    if (block_size != kKTile) {
+    if (block_size != kPoolBlock) {
       set_error("fi_flash_attention_fwd: fused pool write needs block_size %d (got %lld)",
-                kKTile, (long long)block_size);
+                kPoolBlock, (long long)block_size);
       return FI_ERR_UNSUPPORTED;
     }
     if (((uintptr_t)k_cache | (uintptr_t)v_cache) & 15u) {
