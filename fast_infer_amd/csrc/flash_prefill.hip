@@ -3,41 +3,41 @@
 // Replaces _flash_attn_fwd (kernels/attention.py:8-77) and its launcher (:80-113).
 // Same result — softmax(Q K^T * sm_scale, causal) V per query head, fp32 online
 // softmax, fp16 output — but laid out for MI355X:
-//   * a workgroup (8 waves) owns 128 query positions of up to 3 query heads that share
-//     one kv head, so a K/V tile staged in LDS feeds every head of the GQA group and K/V
-//     are never expanded (the reference call site expands them, model.py:110-111);
+//   * a workgroup (4 waves, one per SIMD) owns 64 query positions of up to 3 query heads
+//     that share one kv head, so a K/V tile staged in LDS feeds every head of the GQA
+//     group and K/V are never expanded (the reference call site expands them,
+//     model.py:110-111).  Two workgroups share a CU: the two waves on a SIMD belong to
+//     different workgroups, so neither waits at the other's barriers;
 //   * the grid covers (query tile, head group, batch) with the heaviest causal tiles
 //     dispatched first, instead of one program walking a whole head (:34);
 //   * S^T = K Q^T and O^T = V^T P^T run on v_mfma_f32_16x16x32_f16: the lane holding a
 //     query column keeps its scores, P and O in registers with no shuffles between the
 //     two products; K fragments are read from LDS as A operands and V^T fragments with
 //     the LDS transpose read (ds_read_b64_tr_b16);
-//   * 128-key K/V tiles are copied global->LDS by the buffer unit (no register staging),
-//     double-buffered so the next tile's copy is in flight during the current tile;
+//   * 64-key K/V tiles are copied global->LDS by the buffer unit (no register staging),
+//     double-buffered; each slice issues its share of the next tile's copy;
 //   * the diagonal tile is processed first; when a pool is given, the workgroup that
-//     owns a tile of K/V also copies its two 64-token blocks into the paged pool (the
-//     write of model.py:176-183), so the scatter costs no extra read.
+//     owns a 64-token block of K/V also copies it into the paged pool (the write of
+//     model.py:176-183), so the scatter costs no extra read.
 #include "common.h"
 
 namespace fi {
 namespace prefill {
 
-constexpr int kWaves = 8;                        // two waves per SIMD
+constexpr int kWaves = 4;                        // one wave per SIMD; two workgroups per CU
 constexpr int kThreads = kWaves * 64;
 constexpr int kRowsPerWave = 16;                 // query positions per wave
-constexpr int kQTile = kWaves * kRowsPerWave;    // query positions per workgroup (128)
-constexpr int kKTile = 128;                      // keys per K/V tile (two pool blocks)
+constexpr int kQTile = kWaves * kRowsPerWave;    // query positions per workgroup (64)
+constexpr int kKTile = 64;                       // keys per K/V tile (one pool block)
 constexpr int kPoolBlock = 64;                   // block_size of the fused pool write
 constexpr int kRowBytes = kHeadDim * 2;          // one K or V row in LDS (256 bytes)
 constexpr int kTileBytes = kKTile * kRowBytes;   // 16 KiB
-constexpr int kStageBytes = 2 * kTileBytes;      // K tile + V tile (2 stages: 128 KiB)
-constexpr int kRowsPerWaveLoad = kKTile / kWaves;  // K (and V) tile rows each wave loads
-constexpr int kChunks = kKTile * 16 / kThreads;     // 16-byte chunks of K (and V) per thread
+constexpr int kStageBytes = 2 * kTileBytes;      // K tile + V tile (2 stages: 64 KiB)
 constexpr int kOutOfRange = 0x7ffffff0;          // buffer offset past any tensor: loads give 0
 constexpr int kBufferWord3 = 0x00020000;
 constexpr float kLazyLog2 = 8.f;  // the reference max may lag the true max by 2^8
 
-static_assert(kQTile % kKTile == 0, "query tiles cover whole key tiles");
+static_assert(kQTile == kKTile, "a query tile has exactly one diagonal key tile");
 static_assert(kKTile % kPoolBlock == 0, "a key tile covers whole pool blocks");
 
 struct Params {
@@ -55,6 +55,7 @@ struct Params {
   int hg_per_kv;     // workgroups per kv head (group / heads per workgroup)
   float scale_log2;  // |sm_scale| * log2(e)
   float lazy_raw;    // kLazyLog2 / scale_log2: slack of the reference max in raw units
+  float lazy_log2;   // lazy_raw * scale_log2 (about kLazyLog2)
   uint32_t q_sign;   // 0x80008000 when sm_scale < 0: Q is negated instead of the scale
   int num_q_tiles;
   int k_records;     // bytes addressable from one (batch, kv head) base of k
@@ -69,13 +70,22 @@ struct Params {
   int max_blocks_per_seq;
 };
 
-// Byte address in a K or V LDS tile of 16-byte chunk c (0..15) of row r: rows are
-// 256 bytes, chunks XOR-swizzled by f(r) = ((r & 7) << 1) | ((r >> 3) & 1), a bijection
-// on r & 15.  16 consecutive rows read at one column (K fragments) hit 16 different
-// chunk slots, and the 32-byte pair a transposed V read takes from each of 8
-// consecutive rows lands in 8 different pair slots (f's pair index is r & 7).
-__device__ __forceinline__ int swz(int r, int c) {
-  return r * kRowBytes + ((c ^ (((r & 7) << 1) | ((r >> 3) & 1))) << 4);
+// LDS tile layouts ("panels"): a K tile is 4 panels of 64 bytes per key (head_dim
+// columns 32i..32i+31 in panel i), a V tile 8 panels of 32 bytes per key (columns
+// 16dt..16dt+15 in panel dt).  Every MFMA fragment read then takes one base register
+// per lane plus an immediate offset.  LDS serves a 16-byte read 16 lanes at a time: a
+// K fragment read has 16 consecutive keys at one chunk, so the four 16-byte chunks of
+// key r are stored XOR-permuted by (r >> 2) & 3, which spreads the 16 keys over all 16
+// slots of a 256-byte bank window.  A V^T fragment read (8 bytes, 32 lanes at a time)
+// covers 8 consecutive keys x 32 bytes, one whole window.  Byte offset of 16-byte
+// chunk ch (0..15) of key row r:
+constexpr int kKPanel = kKTile * 64;  // bytes per K panel
+constexpr int kVPanel = kKTile * 32;  // bytes per V panel
+__device__ __forceinline__ int k_off(int r, int ch) {
+  return (ch >> 2) * kKPanel + r * 64 + (((ch & 3) ^ ((r >> 2) & 3)) << 4);
+}
+__device__ __forceinline__ int v_off(int r, int ch) {
+  return (ch >> 1) * kVPanel + r * 32 + ((ch & 1) << 4);
 }
 
 // Wait until at most `n` of this wave's vector-memory operations are outstanding
@@ -86,32 +96,51 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-// Issue the direct-to-LDS loads of this wave's rows of the K/V tile at key k0 into
-// `stage` (K at +0, V at +kTileBytes).  One instruction moves 4 rows (64 lanes x 16
-// bytes) to 1 KiB of consecutive LDS; lane l fills swizzled position l%16 of row
-// 4q + l/16, so it fetches global chunk (l%16) ^ f(row) (see swz).  Rows past seq_len, or a
-// tile past the end (k0 < 0), fetch zeros through the buffer bounds check.
+// Issue the direct-to-LDS loads of this wave's share of the K/V tile at key k0 into
+// `stage` (K at +0, V at +kTileBytes).  One instruction moves 64 lanes x 16 bytes to
+// 1 KiB of consecutive LDS: for K, 16 keys of one panel (lane l: key l/4, chunk
+// 4*panel + l%4); for V, 32 keys of one panel (lane l: key l/2, chunk 2*panel + l%2).
+// Wave w's K instructions cover keys 16w..16w+15 in all four panels and its V
+// instructions keys 32(w/2).. in four of the eight panels, so the lines a wave touches
+// are reused across its own back-to-back instructions.  Keys past seq_len, or a tile
+// past the end (k0 < 0), fetch zeros through the buffer bounds check.
+template <int NW = kWaves>
+__device__ __forceinline__ void issue_tile_part(const Params& p, __amdgpu_buffer_rsrc_t kr,
+                                                __amdgpu_buffer_rsrc_t vr, char* stage, int k0,
+                                                int w, int lane, int q) {
+  typedef void __attribute__((address_space(3))) lds_void;
+  constexpr int kPer = (kTileBytes / 1024) / NW;  // instructions per wave per tensor
+  const int n = kPer * w + q;  // instruction index within the tile (uniform)
+  {
+    // slot l holds key row0 + l/4 at permuted position l%4: logical chunk
+    // (l % 4) ^ ((l / 16) % 4) of the panel (see k_off; row0 is a multiple of 16)
+    const int panel = n & 3, row0 = 16 * (n >> 2);
+    const int key = k0 + row0 + (lane >> 2);
+    const bool ok = k0 >= 0 && key < p.seq_len;
+    const int ch = 4 * panel + ((lane & 3) ^ ((lane >> 4) & 3));
+    const int off = ok ? key * p.k_row_bytes + (ch << 4) : kOutOfRange;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        kr, (lds_void*)(stage + panel * kKPanel + row0 * 64), 16, off, 0, 0, 0);
+  }
+  {
+    const int panel = n & 7, row0 = 32 * (n >> 3);
+    const int key = k0 + row0 + (lane >> 1);
+    const bool ok = k0 >= 0 && key < p.seq_len;
+    const int off = ok ? key * p.v_row_bytes + ((2 * panel + (lane & 1)) << 4) : kOutOfRange;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        vr, (lds_void*)(stage + kTileBytes + panel * kVPanel + row0 * 32), 16, off, 0, 0, 0);
+  }
+}
 template <int NW = kWaves>
 __device__ __forceinline__ void issue_tile(const Params& p, __amdgpu_buffer_rsrc_t kr,
                                            __amdgpu_buffer_rsrc_t vr, char* stage, int k0,
                                            int w, int lane) {
-  typedef void __attribute__((address_space(3))) lds_void;
-  constexpr int kRows = kKTile / NW;  // K (and V) rows this wave loads
+  constexpr int kPer = (kTileBytes / 1024) / NW;
+  static_assert(kPer * NW * 1024 == kTileBytes, "tile split across waves");
 #pragma unroll
-  for (int q = 0; q < kRows / 4; ++q) {
-    const int row0 = kRows * w + 4 * q;
-    const int row = row0 + (lane >> 4);
-    const int key = k0 + row;
-    const int chunk = (lane & 15) ^ (((row & 7) << 1) | ((row >> 3) & 1));
-    const bool ok = k0 >= 0 && key < p.seq_len;
-    const int ko = ok ? key * p.k_row_bytes + (chunk << 4) : kOutOfRange;
-    const int vo = ok ? key * p.v_row_bytes + (chunk << 4) : kOutOfRange;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (lds_void*)(stage + row0 * kRowBytes), 16, ko, 0, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, (lds_void*)(stage + kTileBytes + row0 * kRowBytes), 16,
-                                             vo, 0, 0, 0);
-  }
+  for (int q = 0; q < kPer; ++q) issue_tile_part<NW>(p, kr, vr, stage, k0, w, lane, q);
 }
-constexpr int kIssuePerTile = 2 * (kRowsPerWaveLoad / 4);  // DMA instructions per wave per tile
+constexpr int kIssuePerTile = 2 * (kTileBytes / 1024) / kWaves;  // DMA instructions per wave per tile
 
 // Copy a resident tile (keys k0..k0+kKTile-1, whole pool blocks of 64) from LDS into
 // the pool.
@@ -131,8 +160,8 @@ __device__ __forceinline__ void write_pool(const Params& p, const char* stage, i
     if (phys < 0 || phys >= p.num_pool_blocks) continue;
     const int64_t dst = (phys * kPoolBlock + key % kPoolBlock) * row_stride +
                         (int64_t)kvh * kHeadDim + 8 * (f & 15);
-    *(u32x4*)(p.k_cache + dst) = *(const u32x4*)(stage + swz(slot, f & 15));
-    *(u32x4*)(p.v_cache + dst) = *(const u32x4*)(stage + kTileBytes + swz(slot, f & 15));
+    *(u32x4*)(p.k_cache + dst) = *(const u32x4*)(stage + k_off(slot, f & 15));
+    *(u32x4*)(p.v_cache + dst) = *(const u32x4*)(stage + kTileBytes + v_off(slot, f & 15));
   }
 }
 
@@ -142,9 +171,7 @@ __device__ __forceinline__ void write_pool(const Params& p, const char* stage, i
 // lane 4j + i/4's 4-element chunk to lane i as element j).
 __device__ __forceinline__ u32x2 vt_read(const char* vs, int row0, int dt, int col, int g) {
   typedef short s4 __attribute__((ext_vector_type(4)));
-  const int row = row0 + 4 * g + (col >> 2);
-  const int chunk = 2 * dt + ((col & 3) >> 1);
-  const char* ptr = vs + swz(row, chunk) + ((col & 1) << 3);
+  const char* ptr = vs + dt * kVPanel + (row0 + 4 * g + (col >> 2)) * 32 + ((col & 3) << 3);
   const s4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((s4 __attribute__((address_space(3)))*)ptr);
   return __builtin_bit_cast(u32x2, v);
 }
@@ -164,81 +191,169 @@ __device__ __forceinline__ void pv_half8(const char* vs, int c, int col, int g,
   }
 }
 
-// One key tile: for each 32-key half, S^T = K Q^T, the online softmax, and PV.
+// S^T = K Q^T for 32-key slice c of a resident K tile: s[j][t] holds keys
+// 32c + 16t + 4g + r (tile-relative) for query column col of head j.
 template <int HPW>
-__device__ __forceinline__ void consume_tile(const Params& p, const char* stage, int k0,
-                                             bool diag, int qpos, int wave_last, int col,
-                                             int g, const half8 (&qf)[HPW][4],
-                                             float (&m_run)[HPW], float (&l_run)[HPW],
-                                             floatx4 (&acc)[HPW][8]) {
-  const char* ks = stage;
-  const char* vs = stage + kTileBytes;
-  const float c2 = p.scale_log2;  // > 0; the running max m is kept in raw score units
+__device__ __forceinline__ void qk_slice(const char* ks, int c, int col, int g,
+                                         const half8 (&qf)[HPW][4], floatx4 (&s)[HPW][2]) {
 #pragma unroll
-  for (int c = 0; c < kKTile / 32; ++c) {  // 32-key slices
-    if (diag && k0 + 32 * c > wave_last) break;  // slices wholly above this wave's diagonal
-    // S^T = K Q^T: s[j][t] holds keys k0 + 32c + 16t + 4g + r for query column col.
-    floatx4 s[HPW][2];
+  for (int j = 0; j < HPW; ++j) s[j][0] = s[j][1] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < HPW; ++j) s[j][0] = s[j][1] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < 2; ++t) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
+    for (int i = 0; i < 4; ++i) {
+      const half8 kf = as_half8(*(const u32x4*)(ks + i * kKPanel + (32 * c + 16 * t + col) * 64 +
+                                                 ((g ^ ((col >> 2) & 3)) << 4)));
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const half8 kf = as_half8(*(const u32x4*)(ks + swz(32 * c + 16 * t + col, 4 * i + g)));
-#pragma unroll
-        for (int j = 0; j < HPW; ++j) s[j][t] = mfma16x16x32(kf, qf[j][i], s[j][t]);
-      }
+      for (int j = 0; j < HPW; ++j) s[j][t] = mfma16x16x32(kf, qf[j][i], s[j][t]);
     }
-    // Online softmax per head with a lazily moved reference max m (raw score units):
-    // p = exp2(s*c2 - m*c2).  m only moves when some score exceeds it by more than
-    // kLazyLog2 in the log2 domain, so p <= 2^kLazyLog2 (exact in fp16, O and l in fp32)
-    // and the softmax is unchanged; the test needs no cross-lane step, and the row max
-    // is reduced across the column's four lanes only when m moves.  l accumulates the
-    // fp16 p that the PV product uses (v_dot2_f32_f16 against ones).
-    half8 pf[HPW];
+  }
+}
+
+// This lane's maximum over its 8 scores of each head.
+template <int HPW>
+__device__ __forceinline__ void lane_max(const floatx4 (&s)[HPW][2], float (&lmax)[HPW]) {
+#pragma unroll
+  for (int j = 0; j < HPW; ++j) {
+    float x = fmaxf(fmaxf(fmaxf(s[j][0][0], s[j][0][1]), s[j][0][2]), s[j][0][3]);
+    lmax[j] = fmaxf(fmaxf(fmaxf(fmaxf(x, s[j][1][0]), s[j][1][1]), s[j][1][2]), s[j][1][3]);
+  }
+}
+
+// Online softmax with a lazily moved reference max m (raw score units):
+// p = exp2(s*c2 - m*c2).  m only moves when some score exceeds it by more than
+// kLazyLog2 in the log2 domain, so p <= 2^kLazyLog2 (exact in fp16, O and l in fp32) and
+// the softmax is unchanged.  The running state is the threshold t = m + lazy_raw, so the
+// test is one compare with no cross-lane step; when any lane's test fires (rare after
+// the first slices), every head's row max is reduced across the column's four lanes
+// and O and l are rescaled (alpha == 1 for heads whose threshold stays).
+template <int HPW>
+__device__ __forceinline__ void maybe_move_max(const Params& p, const float (&lmax)[HPW],
+                                               float (&t_run)[HPW], float (&l_run)[HPW],
+                                               floatx4 (&acc)[HPW][8]) {
+  bool move = false;
+#pragma unroll
+  for (int j = 0; j < HPW; ++j) move |= lmax[j] > t_run[j];
+  if (__builtin_amdgcn_ballot_w64(move)) {
 #pragma unroll
     for (int j = 0; j < HPW; ++j) {
-      if (diag) {
+      const float t_old = t_run[j];
+      const float rmax = row4_max(lmax[j]);
+      const float t_new = rmax > t_old ? rmax + p.lazy_raw : t_old;
+      const float alpha = fast_exp2((t_old - t_new) * p.scale_log2);
+      t_run[j] = t_new;
+      l_run[j] *= alpha;
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+      for (int dt = 0; dt < 8; ++dt) acc[j][dt] *= alpha;
+    }
+  }
+}
+
+// P = exp2(s*c2 - m*c2) rounded to fp16 (the PV operand).
+template <int HPW>
+__device__ __forceinline__ void softmax_exp(const Params& p, const floatx4 (&s)[HPW][2],
+                                            const float (&t_run)[HPW], half8 (&pf)[HPW]) {
+  const float c2 = p.scale_log2;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int key = k0 + 32 * c + 16 * t + 4 * g + r;
-            if (key > qpos || key >= p.seq_len) s[j][t][r] = -__builtin_inff();
-          }
-      }
-      float lmax = fmaxf(fmaxf(fmaxf(s[j][0][0], s[j][0][1]), s[j][0][2]), s[j][0][3]);
-      lmax = fmaxf(fmaxf(fmaxf(fmaxf(lmax, s[j][1][0]), s[j][1][1]), s[j][1][2]), s[j][1][3]);
-      if (__builtin_amdgcn_ballot_w64(lmax > m_run[j] + p.lazy_raw)) {
-        const float m_old = m_run[j];
-        const float rmax = row4_max(lmax);
-        const float m_new = rmax > m_old + p.lazy_raw ? rmax : m_old;
-        const float alpha = fast_exp2((m_old - m_new) * c2);
-        m_run[j] = m_new;
-        l_run[j] *= alpha;
+  for (int j = 0; j < HPW; ++j) {
+    const float mc = __builtin_fmaf(t_run[j], c2, -p.lazy_log2);  // m * c2
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) acc[j][dt] *= alpha;
-      }
-      const float mc = m_run[j] * c2;
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        pf[j][4 * t + r] = (half_t)fast_exp2(__builtin_fmaf(s[j][t][r], c2, -mc));
+  }
+}
+
+// P as above, and l accumulates those fp16 values (v_dot2_f32_f16 against ones).
+template <int HPW>
+__device__ __forceinline__ void softmax_p(const Params& p, const floatx4 (&s)[HPW][2],
+                                          const float (&m_run)[HPW], float (&l_run)[HPW],
+                                          half8 (&pf)[HPW]) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  softmax_exp<HPW>(p, s, m_run, pf);
+  const h2 one2 = {(half_t)1.f, (half_t)1.f};
+#pragma unroll
+  for (int j = 0; j < HPW; ++j) {
+    float psum = l_run[j];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      psum = __builtin_amdgcn_fdot2(h2{pf[j][2 * e], pf[j][2 * e + 1]}, one2, psum, false);
+    l_run[j] = psum;
+  }
+}
+
+// A tile on the diagonal: masked (key > position, key >= seq_len), slices wholly above
+// this wave's last position skipped; one slice at a time.
+template <int HPW>
+__device__ __forceinline__ void consume_diag(const Params& p, const char* stage, int k0,
+                                             int qpos, int wave_last, int col, int g,
+                                             const half8 (&qf)[HPW][4], float (&m_run)[HPW],
+                                             float (&l_run)[HPW], floatx4 (&acc)[HPW][8]) {
+  const char* ks = stage;
+  const char* vs = stage + kTileBytes;
+#pragma unroll
+  for (int c = 0; c < kKTile / 32; ++c) {
+    if (k0 + 32 * c > wave_last) break;
+    floatx4 s[HPW][2];
+    qk_slice<HPW>(ks, c, col, g, qf, s);
+#pragma unroll
+    for (int j = 0; j < HPW; ++j)
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) pf[j][4 * t + r] = (half_t)fast_exp2(__builtin_fmaf(s[j][t][r], c2, -mc));
-      typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-      const h2 one2 = {(half_t)1.f, (half_t)1.f};
-      float psum = l_run[j];
+        for (int r = 0; r < 4; ++r) {
+          const int key = k0 + 32 * c + 16 * t + 4 * g + r;
+          if (key > qpos || key >= p.seq_len) s[j][t][r] = -__builtin_inff();
+        }
+    float lmax[HPW];
+    lane_max<HPW>(s, lmax);
+    maybe_move_max<HPW>(p, lmax, m_run, l_run, acc);
+    half8 pf[HPW];
+    softmax_p<HPW>(p, s, m_run, l_run, pf);
+    pv_half8<HPW>(vs, c, col, g, pf, acc);
+  }
+}
+
+
+// A tile wholly below the diagonal: per 32-key slice, QK for every head of the group
+// (each K fragment read once), the online softmax, then PV (each V^T fragment read
+// once).  No masking.
+template <int HPW>
+__device__ __forceinline__ void consume_full(const Params& p, const char* stage, int col,
+                                             int g, const half8 (&qf)[HPW][4],
+                                             float (&m_run)[HPW], float (&l_run)[HPW],
+                                             floatx4 (&acc)[HPW][8], __amdgpu_buffer_rsrc_t kr,
+                                             __amdgpu_buffer_rsrc_t vr, char* nxt, int k0n,
+                                             int w, int lane) {
+  const char* ks = stage;
+  const char* vs = stage + kTileBytes;
+  constexpr int kPer = (kTileBytes / 1024) / kWaves;  // copy instruction pairs per wave
+  constexpr int kPerSlice = kPer / (kKTile / 32);
+  static_assert(kPerSlice * (kKTile / 32) == kPer, "copy instructions split evenly over slices");
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        psum = __builtin_amdgcn_fdot2(h2{pf[j][2 * e], pf[j][2 * e + 1]}, one2, psum, false);
-      l_run[j] = psum;
-    }
+  for (int c = 0; c < kKTile / 32; ++c) {
+    // A uniform branch between slices (never taken) keeps the compiler from treating
+    // the unrolled slices as one straight-line region, which otherwise overlaps them
+    // far beyond the register file and spills.
+    if (p.seq_len < 0) break;
+    floatx4 s[HPW][2];
+    qk_slice<HPW>(ks, c, col, g, qf, s);
+    // this slice's share of the next tile's copy, issued while the QK MFMAs run (all
+    // waves issuing a whole tile at once would queue behind each other)
+#pragma unroll
+    for (int q = 0; q < kPerSlice; ++q) issue_tile_part(p, kr, vr, nxt, k0n, w, lane, kPerSlice * c + q);
+    float lmax[HPW];
+    lane_max<HPW>(s, lmax);
+    maybe_move_max<HPW>(p, lmax, m_run, l_run, acc);
+    half8 pf[HPW];
+    softmax_p<HPW>(p, s, m_run, l_run, pf);
     pv_half8<HPW>(vs, c, col, g, pf, acc);
   }
 }
 
 template <int HPW>  // query heads per workgroup
-__global__ __launch_bounds__(kThreads) void fwd_kernel(Params p) {
+__global__ __launch_bounds__(kThreads, 2) void fwd_kernel(Params p) {
   // two pipeline stages of one K tile + one V tile each (distinct objects, so the
   // compiler tracks their DMA writes separately)
   __shared__ __attribute__((aligned(16))) char st0[kStageBytes];
@@ -290,41 +405,40 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(Params p) {
     for (int dt = 0; dt < 8; ++dt) acc[j][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
 
-  // Key tiles: the diagonal tiles (those holding this workgroup's own positions) first,
-  // then tiles 0, 1, ... before the diagonal.
-  const int total_kt = (p.seq_len + kKTile - 1) / kKTile;
-  const int kt_diag0 = q0 / kKTile;
-  const int n_diag = min(kQTile / kKTile, total_kt - kt_diag0);
-  const int n = kt_diag0 + n_diag;
+  // Key tiles: the diagonal tile (keys q0..q0+kKTile-1, this workgroup's own positions)
+  // first, then tiles 0, 1, ... before it.
+  const int n = qt + 1;
   auto key0 = [&](int idx) -> int {
     if (idx >= n) return -1;  // past the end: loads read zeros
-    return (idx < n_diag ? kt_diag0 + idx : idx - n_diag) * kKTile;
+    return (idx == 0 ? qt : idx - 1) * kKTile;
   };
   const bool pool = p.k_cache != nullptr && hsub == 0;
   const int wave_last = q0 + kRowsPerWave * w + kRowsPerWave - 1;  // last position of the wave
 
-  // Two-stage pipeline over 128-key tiles (tile idx in stage idx % 2): issue the DMA of
-  // tile idx+1 into the other stage (its last reader finished before the previous
-  // barrier), consume tile idx, wait for this wave's DMA of tile idx+1, barrier.
-#define FI_PREFILL_STEP(IDX, CUR, NXT)                                                   \
-  {                                                                                      \
-    const int i_ = (IDX);                                                                \
-    issue_tile(p, kr, vr, NXT, key0(i_ + 1), w, lane);                                   \
-    const int k0 = key0(i_);                                                             \
-    const bool diag = i_ < n_diag;                                                       \
-    if (diag && pool) write_pool(p, CUR, b, kvh, k0, tid);                               \
-    consume_tile<HPW>(p, CUR, k0, diag, qpos, wave_last, col, g, qf, m_run, l_run, acc); \
-    wait_vmcnt<0>();                                                                     \
-    __builtin_amdgcn_s_barrier();                                                        \
-  }
-
+  // Two-stage pipeline over 128-key tiles (tile idx in stage idx % 2): while consuming
+  // tile idx, copy tile idx+1 into the other stage (its last reader finished before the
+  // previous barrier), then wait for this wave's copies and barrier.  Tile 0 is the
+  // diagonal tile (masked; copied to the pool when one is given), the others lie wholly
+  // below the diagonal.
   issue_tile(p, kr, vr, st0, key0(0), w, lane);
   wait_vmcnt<0>();
   __builtin_amdgcn_s_barrier();
-  for (int idx = 0; idx < n; idx += 2) {
-    FI_PREFILL_STEP(idx, st0, st1)
+  issue_tile(p, kr, vr, st1, key0(1), w, lane);
+  if (pool) write_pool(p, st0, b, kvh, key0(0), tid);
+  consume_diag<HPW>(p, st0, key0(0), qpos, wave_last, col, g, qf, m_run, l_run, acc);
+  wait_vmcnt<0>();
+  __builtin_amdgcn_s_barrier();
+#define FI_PREFILL_STEP(IDX, CUR, NXT)                                                    \
+  {                                                                                       \
+    consume_full<HPW>(p, CUR, col, g, qf, m_run, l_run, acc, kr, vr, NXT, key0((IDX) + 1), \
+                      w, lane);                                                           \
+    wait_vmcnt<0>();                                                                      \
+    __builtin_amdgcn_s_barrier();                                                         \
+  }
+  for (int idx = 1; idx < n; idx += 2) {
+    FI_PREFILL_STEP(idx, st1, st0)
     if (idx + 1 >= n) break;
-    FI_PREFILL_STEP(idx + 1, st1, st0)
+    FI_PREFILL_STEP(idx + 1, st0, st1)
   }
 #undef FI_PREFILL_STEP
 
@@ -426,6 +540,7 @@ extern "C" int fi_flash_attention_fwd(const void* q, const void* k, const void* 
   p.scale_log2 = (sm_scale < 0 ? -sm_scale : sm_scale) * kLog2e;
   p.q_sign = sm_scale < 0 ? 0x80008000u : 0u;
   p.lazy_raw = p.scale_log2 > 0.f ? kLazyLog2 / p.scale_log2 : 0.f;
+  p.lazy_log2 = p.lazy_raw * p.scale_log2;
   p.num_q_tiles = (int)((seq_len + kQTile - 1) / kQTile);
   p.k_cache = (half_t*)k_cache;
   p.v_cache = (half_t*)v_cache;
