@@ -9,10 +9,13 @@
 //   * the context is split into partitions (flash-decoding); each workgroup turns one
 //     partition into an unnormalised partial (m, l, o) and a second small kernel
 //     merges the partials; a single-partition call writes the output directly;
-//   * QK^T and PV run on MFMA (v_mfma_f32_16x16x32_f16) with the GQA heads as the
-//     16-wide N dimension: S^T = K * Q^T takes K rows straight from HBM into the A
-//     fragment (16-byte loads), and O^T = V^T * P^T reads V^T from a wave-private
-//     LDS tile that the wave fills with a register transpose.
+//   * each wave streams 16-token K and V tiles global->LDS with the buffer unit (no
+//     register staging, whole 256-byte rows per request), double-buffered in a
+//     wave-private LDS region, so many loads stay in flight at low register cost;
+//   * QK^T and PV run on MFMA with the GQA heads as the 16-wide N dimension:
+//     S^T = K * Q^T (v_mfma_f32_16x16x32_f16, K fragments read from LDS) and
+//     O^T = V^T * P^T (v_mfma_f32_16x16x16_f16, V^T fragments from the LDS transpose
+//     read ds_read_b64_tr_b16, P^T straight from the S^T accumulator lanes).
 //   * Online softmax is fp32 in log2 units (exp2 with sm_scale * log2(e) folded in).
 #include "common.h"
 
@@ -20,23 +23,24 @@ namespace fi {
 
 namespace decode {
 
-constexpr int kWaves = 4;                        // waves per workgroup
-constexpr int kIterTokens = 32;                  // tokens per wave per iteration
-constexpr int kWgTokens = kWaves * kIterTokens;  // tokens per workgroup iteration
-constexpr int kVtStride = kIterTokens + 4;       // fp16 per V^T row in LDS (bank padding)
-constexpr int kVtHalfs = kHeadDim * kVtStride;   // one wave's V^T tile
-constexpr int kMaxHeadsPerWg = 16;               // MFMA N dimension
-constexpr int kCmbStride = kHeadDim + 4;         // floats per merged row (bank padding)
-constexpr int kSmemBytes = kWaves * kVtHalfs * 2;
+constexpr int kWaves = 4;                          // waves per workgroup
+constexpr int kTileTokens = 16;                    // tokens per wave tile (one MFMA tile)
+constexpr int kWgTokens = kWaves * kTileTokens;    // tokens per workgroup round
+constexpr int kTileBytes = kTileTokens * kHeadDim * 2;  // one K (or V) tile in LDS: 4 KiB
+constexpr int kBufBytes = 2 * kTileBytes;          // K + V tile of one wave
+constexpr int kMaxHeadsPerWg = 16;                 // MFMA N dimension
 constexpr int kMaxSplitTokens = 4096;                       // cap on the partition size
 constexpr int kMaxSplitEntries = kMaxSplitTokens / 16 + 1;  // table entries of a partition
 constexpr int kMaxSplits = 1024;                            // partitions per row
 constexpr int kOutOfRange = 0x40000000;  // buffer offset beyond any block: loads return 0
 constexpr int kBufferWord3 = 0x00020000;  // raw buffer: 32-bit data format, no swizzle
+// Cache policy of the K/V loads: non-temporal (each byte is read once per call; not
+// allocating it in L2 streams measurably faster than default-policy loads).
+constexpr int kStreamPolicy = 2;
 
-static_assert(kWaves * kMaxHeadsPerWg * kCmbStride * 4 + kWaves * kMaxHeadsPerWg * 2 * 4 <=
-                  kSmemBytes,
-              "merge area must fit in the V^T tiles");
+// the wave merge reuses one tile buffer array: [wave][head][128] fp32
+static_assert(kWaves * kMaxHeadsPerWg * kHeadDim * 4 <= kWaves * kBufBytes,
+              "merge area must fit in one buffer array");
 
 struct Params {
   const half_t* q;
@@ -72,13 +76,6 @@ __device__ __forceinline__ int row_context(const Params& p, int b) {
   return ctx < 0 ? 0 : ctx;
 }
 
-// Registers of one wave iteration: 32 tokens as two 16-token tiles.
-struct IterRegs {
-  u32x4 kf[2][4];  // K A-fragments: lane (col, g) holds token tile+col, d = 32i + 8g..+7
-  u32x4 vr[2][4];  // V rows: lane (dc, kq) holds token tile + 4kq + j, d = 8dc..8dc+7
-  bool ok[2];      // tile inside the partition and mapped to a pool block
-};
-
 // Buffer descriptor covering one kv head's rows of one pool block; a block outside the
 // pool gets zero records, so every load through it returns 0 without touching memory.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t block_rsrc(const half_t* pool, int64_t phys,
@@ -89,113 +86,104 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t block_rsrc(const half_t* pool,
                                            ok ? (int)(block_bytes - kv_off) : 0, kBufferWord3);
 }
 
-// Issue the global loads of the wave iteration starting at token `base`.  Lanes whose
-// token is outside [.., split_end) get an out-of-range offset and read zeros.
-__device__ __forceinline__ void issue_iter(const Params& p, const int* s_tab, int tab0,
-                                           int base, int split_end, int kv_off,
-                                           int64_t block_bytes, int row_bytes, int col, int g,
-                                           int dc, int kq, IterRegs& r) {
+// LDS tile layout: 16 rows (tokens) of 256 bytes.  K row r keeps 16-byte chunk c at slot
+// c ^ r, so the 16 lanes of a K fragment read (16 rows, one chunk) hit 16 distinct bank
+// slots.  V row r keeps chunk c at slot c ^ 2(r % 8), so the 32-byte column pairs a
+// transpose read takes from 8 consecutive rows land in 8 distinct pair slots.
+__device__ __forceinline__ int kslot(int r, int c) { return r * 256 + ((c ^ r) << 4); }
+__device__ __forceinline__ int vslot(int r, int c) { return r * 256 + ((c ^ ((r & 7) << 1)) << 4); }
+
+// Issue the direct-to-LDS loads of one 16-token tile (tokens tile..tile+15 of the row)
+// into buf (K at +0, V at +kTileBytes).  One instruction moves 4 rows; lane l fills slot
+// l % 16 of row 4q + l / 16 and so fetches the chunk stored there.  Tokens at or past
+// split_end, and tiles whose table entry is outside the pool, read zeros.
+__device__ __forceinline__ bool issue_tile(const Params& p, const int* s_tab, int tab0,
+                                           int tile, int split_end, int kv_off,
+                                           int64_t block_bytes, int row_bytes, char* buf,
+                                           int lane) {
+  typedef void __attribute__((address_space(3))) lds_void;
+  int64_t phys = -1;
+  if (tile < split_end) phys = __builtin_amdgcn_readfirstlane(s_tab[tile / p.block_size - tab0]);
+  const __amdgpu_buffer_rsrc_t kr = block_rsrc(p.k_cache, phys, block_bytes, kv_off);
+  const __amdgpu_buffer_rsrc_t vr = block_rsrc(p.v_cache, phys, block_bytes, kv_off);
+  const int slot0 = tile % p.block_size;  // 16-token tiles never straddle a block
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int tile = base + 16 * t;  // 16-token tiles never straddle a block
-    int64_t phys = -1;
-    if (tile < split_end) phys = __builtin_amdgcn_readfirstlane(s_tab[tile / p.block_size - tab0]);
-    r.ok[t] = phys >= 0;
-    const __amdgpu_buffer_rsrc_t kr = block_rsrc(p.k_cache, phys, block_bytes, kv_off);
-    const __amdgpu_buffer_rsrc_t vr = block_rsrc(p.v_cache, phys, block_bytes, kv_off);
-    const int slot = tile % p.block_size;
-    const int koff = tile + col < split_end ? (slot + col) * row_bytes + 16 * g : kOutOfRange;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      r.kf[t][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff + 64 * i, 0, 0));
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int tok = 4 * kq + j;
-      const int voff = tile + tok < split_end ? (slot + tok) * row_bytes + 16 * dc : kOutOfRange;
-      r.vr[t][j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, voff, 0, 0));
-    }
+  for (int q = 0; q < 4; ++q) {
+    const int row = 4 * q + (lane >> 4);
+    const bool in = tile + row < split_end;
+    const int kc = (lane & 15) ^ row;
+    const int vc = (lane & 15) ^ ((row & 7) << 1);
+    const int koff = in ? (slot0 + row) * row_bytes + (kc << 4) : kOutOfRange;
+    const int voff = in ? (slot0 + row) * row_bytes + (vc << 4) : kOutOfRange;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (lds_void*)(buf + q * 1024), 16, koff, 0, 0,
+                                             kStreamPolicy);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, (lds_void*)(buf + kTileBytes + q * 1024), 16,
+                                             voff, 0, 0, kStreamPolicy);
   }
+  return phys >= 0;
+}
+constexpr int kIssuePerTile = 8;  // load instructions per issue_tile
+
+// Wait until at most N of this wave's vector-memory operations are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-// Online-softmax update of one wave iteration (32 tokens at `base`).
-__device__ __forceinline__ void consume_iter(const Params& p, const IterRegs& r, int base,
-                                             int split_end, const half8 (&qf)[4], half_t* vt,
-                                             int col, int g, int dc, int kq, float& m_run,
-                                             float& l_run, floatx4 (&acc)[8]) {
-  // S^T = K * Q^T for the two tiles: lane holds keys 16t + 4g + r of column col.
-  floatx4 s[2];
+// Online-softmax update with one resident 16-token tile at `tile`.
+__device__ __forceinline__ void consume_tile(const Params& p, const char* buf, bool ok, int tile,
+                                             int split_end, const half8 (&qf)[4], int col,
+                                             int g, float& m_run, float& l_run,
+                                             floatx4 (&acc)[8]) {
+  typedef short s4 __attribute__((ext_vector_type(4)));
+  // S^T = K * Q^T: lane holds tokens tile + 4g + r of head column col.
+  floatx4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    floatx4 c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) c = mfma16x16x32(as_half8(r.kf[t][i]), qf[i], c);
-    s[t] = c;
-  }
+  for (int i = 0; i < 4; ++i)
+    s = mfma16x16x32(as_half8(*(const u32x4*)(buf + kslot(col, 4 * i + g))), qf[i], s);
 
-  // Online softmax (log2 domain); tokens past the partition or in a tile whose table
-  // entry is outside the pool are masked to -inf.
+  float x[4];
   float tmax = kNegBig;
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int tok = base + 16 * t + 4 * g + i;
-      const float x = (r.ok[t] && tok < split_end) ? s[t][i] * p.scale_log2 : -__builtin_inff();
-      s[t][i] = x;
-      tmax = fmaxf(tmax, x);
-    }
+  for (int r = 0; r < 4; ++r) {
+    const int tok = tile + 4 * g + r;
+    x[r] = (ok && tok < split_end) ? s[r] * p.scale_log2 : -__builtin_inff();
+    tmax = fmaxf(tmax, x[r]);
   }
   tmax = row4_max(tmax);
   const float m_new = fmaxf(m_run, tmax);
   const float alpha = fast_exp2(m_run - m_new);
   m_run = m_new;
+  half4 pf;
   float psum = 0.f;
-  half8 pf;
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float e = fast_exp2(s[t][i] - m_new);
-      psum += e;
-      pf[4 * t + i] = (half_t)e;
-    }
+  for (int r = 0; r < 4; ++r) {
+    const float e = fast_exp2(x[r] - m_new);
+    psum += e;
+    pf[r] = (half_t)e;
   }
   l_run = l_run * alpha + psum;
-#pragma unroll
-  for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
 
-  // V^T into this wave's LDS tile: lane writes rows d = 8dc + e, keys 16t + 4kq..+3.
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-#pragma unroll
-    for (int e2 = 0; e2 < 4; ++e2) {
-      // dword e2 of each key row holds d = 8dc + 2e2 (low half) and + 1 (high half)
-      const u32x2 lo = {pack_lo(r.vr[t][0][e2], r.vr[t][1][e2]), pack_lo(r.vr[t][2][e2], r.vr[t][3][e2])};
-      const u32x2 hi = {pack_hi(r.vr[t][0][e2], r.vr[t][1][e2]), pack_hi(r.vr[t][2][e2], r.vr[t][3][e2])};
-      *(u32x2*)(vt + (8 * dc + 2 * e2) * kVtStride + 16 * t + 4 * kq) = lo;
-      *(u32x2*)(vt + (8 * dc + 2 * e2 + 1) * kVtStride + 16 * t + 4 * kq) = hi;
-    }
-  }
-  wave_lds_sync();
-
-  // O^T += V^T * P^T: A = V^T rows d, slots (keys 4g..4g+3, 16+4g..16+4g+3).
+  // O^T += V^T * P^T (16 keys): lane (col, g) of the transpose read gets keys 4g..4g+3
+  // of head_dim column 16dt + col (row 4g + col/4, columns 16dt + 4(col%4)..+3).
+  const int vrow = 4 * g + (col >> 2);
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) {
-    const half_t* row = vt + (16 * dt + col) * kVtStride;
-    const u32x2 a0 = *(const u32x2*)(row + 4 * g);
-    const u32x2 a1 = *(const u32x2*)(row + 16 + 4 * g);
-    const u32x4 a = {a0[0], a0[1], a1[0], a1[1]};
-    acc[dt] = mfma16x16x32(as_half8(a), pf, acc[dt]);
+    const int c = 2 * dt + ((col & 3) >> 1);
+    const char* ptr = buf + kTileBytes + vslot(vrow, c) + ((col & 1) << 3);
+    const s4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((s4 __attribute__((address_space(3)))*)ptr);
+    acc[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(half4, v), pf,
+                                                    acc[dt] * alpha, 0, 0, 0);
   }
-  wave_lds_sync();
 }
 
-// kPipelined: two register buffers, the next iteration's loads in flight while the
-// current one is consumed (2 waves per SIMD).  Otherwise (the default) one buffer and
-// up to 4 waves per SIMD: more resident waves keep more loads in flight per CU.
-template <bool kPipelined>
-__global__ __launch_bounds__(256, kPipelined ? 2 : 3) void partition_kernel(Params p) {
-  __shared__ __attribute__((aligned(16))) char smem[kSmemBytes];
+__global__ __launch_bounds__(256, 2) void partition_kernel(Params p) {
+  // two tile buffers per wave (distinct objects, so the compiler tracks the copies into
+  // one separately from reads of the other)
+  __shared__ __attribute__((aligned(16))) char buf0[kWaves * kBufBytes];
+  __shared__ __attribute__((aligned(16))) char buf1[kWaves * kBufBytes];
+  __shared__ float s_ml[kWaves * kMaxHeadsPerWg * 2];
   __shared__ int s_tab[kMaxSplitEntries];
 
   const int lane = threadIdx.x & 63;
@@ -233,7 +221,7 @@ __global__ __launch_bounds__(256, kPipelined ? 2 : 3) void partition_kernel(Para
 
   // Q^T fragments (B operand of S^T = K * Q^T): column `col` is query head head0+col;
   // MFMA i takes head_dim d = 32*i + 8*g + s in reduction slot 8*g + s (the K
-  // fragment uses the same map, so lanes g = 0..3 read 64 contiguous bytes).
+  // fragment uses the same map).
   half8 qf[4];
   {
     const bool valid = col < p.heads_per_wg;
@@ -250,9 +238,8 @@ __global__ __launch_bounds__(256, kPipelined ? 2 : 3) void partition_kernel(Para
   const int row_bytes = p.num_kv_heads * kHeadDim * 2;  // one pool slot, all kv heads
   const int64_t block_bytes = (int64_t)p.block_size * row_bytes;
   const int kv_off = kvh * kHeadDim * 2;
-  half_t* vt = (half_t*)smem + w * kVtHalfs;  // this wave's V^T tile [128][kVtStride]
-  const int dc = lane >> 2;  // V loader: 8 head_dim values
-  const int kq = lane & 3;   // V loader: 4 consecutive keys
+  char* wb0 = buf0 + w * kBufBytes;
+  char* wb1 = buf1 + w * kBufBytes;
 
   float m_run = kNegBig;
   float l_run = 0.f;
@@ -260,46 +247,46 @@ __global__ __launch_bounds__(256, kPipelined ? 2 : 3) void partition_kernel(Para
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) acc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  // Two-deep software pipeline: the loads of iteration it+1 are in flight while
-  // iteration it is consumed.  Loads past the partition read zeros (no traffic).
-  const int first = split_start + w * kIterTokens;
-  const int n_it = first < split_end ? (split_end - first + kWgTokens - 1) / kWgTokens : 0;
-  if constexpr (kPipelined) {
-    IterRegs ra, rb;
-    if (n_it > 0)
-      issue_iter(p, s_tab, tab0, first, split_end, kv_off, block_bytes, row_bytes, col, g, dc, kq, ra);
-    for (int it = 0; it < n_it; it += 2) {
-      const int b0 = first + it * kWgTokens;
-      issue_iter(p, s_tab, tab0, b0 + kWgTokens, split_end, kv_off, block_bytes, row_bytes, col,
-                 g, dc, kq, rb);
-      consume_iter(p, ra, b0, split_end, qf, vt, col, g, dc, kq, m_run, l_run, acc);
-      if (it + 1 >= n_it) break;
-      issue_iter(p, s_tab, tab0, b0 + 2 * kWgTokens, split_end, kv_off, block_bytes, row_bytes,
-                 col, g, dc, kq, ra);
-      consume_iter(p, rb, b0 + kWgTokens, split_end, qf, vt, col, g, dc, kq, m_run, l_run, acc);
+  // Wave w takes tiles w, w + kWaves, ... of the partition, double-buffered: the copy of
+  // tile k+1 is in flight while tile k is consumed.
+  const int first = split_start + w * kTileTokens;
+  const int n_t = first < split_end ? (split_end - first + kWgTokens - 1) / kWgTokens : 0;
+  bool ok0 = false, ok1 = false;
+  if (n_t > 0)
+    ok0 = issue_tile(p, s_tab, tab0, first, split_end, kv_off, block_bytes, row_bytes, wb0, lane);
+  for (int k = 0; k < n_t; k += 2) {
+    const int t0 = first + k * kWgTokens;
+    if (k + 1 < n_t) {
+      ok1 = issue_tile(p, s_tab, tab0, t0 + kWgTokens, split_end, kv_off, block_bytes, row_bytes,
+                       wb1, lane);
+      wait_vmcnt<kIssuePerTile>();
+    } else {
+      wait_vmcnt<0>();
     }
-  } else {
-    for (int it = 0; it < n_it; ++it) {
-      const int b0 = first + it * kWgTokens;
-      IterRegs ra;
-      issue_iter(p, s_tab, tab0, b0, split_end, kv_off, block_bytes, row_bytes, col, g, dc, kq, ra);
-      consume_iter(p, ra, b0, split_end, qf, vt, col, g, dc, kq, m_run, l_run, acc);
+    consume_tile(p, wb0, ok0, t0, split_end, qf, col, g, m_run, l_run, acc);
+    if (k + 1 >= n_t) break;
+    if (k + 2 < n_t) {
+      ok0 = issue_tile(p, s_tab, tab0, t0 + 2 * kWgTokens, split_end, kv_off, block_bytes,
+                       row_bytes, wb0, lane);
+      wait_vmcnt<kIssuePerTile>();
+    } else {
+      wait_vmcnt<0>();
     }
+    consume_tile(p, wb1, ok1, t0 + kWgTokens, split_end, qf, col, g, m_run, l_run, acc);
   }
 
   l_run = row4_sum(l_run);
 
-  // ---- merge the four waves through LDS (reuses the V^T area).
+  // ---- merge the four waves through LDS (reuses the first buffer array).
   __syncthreads();
-  float* cmb_o = (float*)smem;                                   // [w][col][kCmbStride]
-  float* cmb_ml = cmb_o + kWaves * kMaxHeadsPerWg * kCmbStride;  // [w][col][2]
+  float* cmb_o = (float*)buf0;  // [w][col][128]
   if (col < p.heads_per_wg) {
-    float* dst = cmb_o + (w * kMaxHeadsPerWg + col) * kCmbStride + 4 * g;
+    float* dst = cmb_o + (w * kMaxHeadsPerWg + col) * kHeadDim + 4 * g;
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) *(floatx4*)(dst + 16 * dt) = acc[dt];
     if (g == 0) {
-      cmb_ml[(w * kMaxHeadsPerWg + col) * 2 + 0] = m_run;
-      cmb_ml[(w * kMaxHeadsPerWg + col) * 2 + 1] = l_run;
+      s_ml[(w * kMaxHeadsPerWg + col) * 2 + 0] = m_run;
+      s_ml[(w * kMaxHeadsPerWg + col) * 2 + 1] = l_run;
     }
   }
   __syncthreads();
@@ -310,15 +297,15 @@ __global__ __launch_bounds__(256, kPipelined ? 2 : 3) void partition_kernel(Para
     float mx = kNegBig;
 #pragma unroll
     for (int ww = 0; ww < kWaves; ++ww) {
-      mw[ww] = cmb_ml[(ww * kMaxHeadsPerWg + c) * 2];
+      mw[ww] = s_ml[(ww * kMaxHeadsPerWg + c) * 2];
       mx = fmaxf(mx, mw[ww]);
     }
     float L = 0.f, O = 0.f;
 #pragma unroll
     for (int ww = 0; ww < kWaves; ++ww) {
       const float sc = fast_exp2(mw[ww] - mx);
-      L += sc * cmb_ml[(ww * kMaxHeadsPerWg + c) * 2 + 1];
-      O += sc * cmb_o[(ww * kMaxHeadsPerWg + c) * kCmbStride + d];
+      L += sc * s_ml[(ww * kMaxHeadsPerWg + c) * 2 + 1];
+      O += sc * cmb_o[(ww * kMaxHeadsPerWg + c) * kHeadDim + d];
     }
     const int h = head0 + c;
     if (p.direct) {
@@ -370,10 +357,11 @@ __global__ __launch_bounds__(kHeadDim) void merge_kernel(Params p) {
 }
 
 // Partition size (tokens, a multiple of kWgTokens) for a call: about kTargetWgs
-// workgroups in total, 128..256 tokens each (short partitions keep every CU streaming
-// at small batch and balance ragged rows; the merge reads ~0.5 KiB per partition and
-// head).  A context that fits in four workgroup iterations is one partition with no
-// merge.  FI_DECODE_TOKENS_PER_SPLIT / FI_DECODE_TARGET_WGS override (tuning sweeps).
+// workgroups in total if every row had the maximum length, 128..384 tokens each (short
+// partitions keep every CU streaming at small batch; longer ones amortise the
+// workgroup's table and merge work; the merge reads ~0.5 KiB per partition and head).
+// A context of at most 512 tokens is one partition with no merge.
+// FI_DECODE_TOKENS_PER_SPLIT / FI_DECODE_TARGET_WGS override (tuning sweeps).
 static int tokens_per_split(int64_t batch, int64_t wg_per_row, int64_t num_tokens) {
   static int env_tps = -1;
   if (env_tps < 0) {
@@ -387,23 +375,23 @@ static int tokens_per_split(int64_t batch, int64_t wg_per_row, int64_t num_token
     env_target = s ? atoi(s) : 0;
     if (env_target < 0) env_target = 0;
   }
-  const int64_t target = env_target > 0 ? env_target : 4096;
+  const int64_t target = env_target > 0 ? env_target : 2048;
   int64_t tps;
   if (env_tps > 0) {
     tps = env_tps;
-  } else if (num_tokens <= 4 * kWgTokens) {
+  } else if (num_tokens <= 512) {
     tps = num_tokens;
   } else {
     const int64_t per_row = batch * wg_per_row;
     int64_t want = (target + per_row - 1) / per_row;
     if (want < 1) want = 1;
     tps = (num_tokens + want - 1) / want;
-    if (tps > 2 * kWgTokens) tps = 2 * kWgTokens;
+    if (tps > 384) tps = 384;
   }
   const int64_t min_tps = (num_tokens + kMaxSplits - 1) / kMaxSplits;
   if (tps < min_tps) tps = min_tps;
   tps = (tps + kWgTokens - 1) / kWgTokens * kWgTokens;
-  if (tps < kWgTokens) tps = kWgTokens;
+  if (tps < 128) tps = 128;
   if (tps > kMaxSplitTokens) tps = kMaxSplitTokens;
   return (int)tps;
 }
@@ -523,16 +511,8 @@ extern "C" int fi_paged_attention_fwd(const void* q, int64_t q_sb, int64_t q_sh,
     set_error("fi_paged_attention_fwd: grid too large");
     return FI_ERR_UNSUPPORTED;
   }
-  static int variant = -1;  // FI_DECODE_VARIANT=1: the 2-deep pipelined kernel (tuning)
-  if (variant < 0) {
-    const char* s = getenv("FI_DECODE_VARIANT");
-    variant = s ? atoi(s) : 0;
-  }
   const dim3 grid((unsigned)wg_per_row, (unsigned)splits, (unsigned)batch);
-  if (variant == 1)
-    hipLaunchKernelGGL(partition_kernel<true>, grid, dim3(kWaves * 64), 0, (hipStream_t)stream, p);
-  else
-    hipLaunchKernelGGL(partition_kernel<false>, grid, dim3(kWaves * 64), 0, (hipStream_t)stream, p);
+  hipLaunchKernelGGL(partition_kernel, grid, dim3(kWaves * 64), 0, (hipStream_t)stream, p);
   int rc = check_launch("fi_paged_attention_fwd(partition)");
   if (rc != FI_OK || p.direct) return rc;
   hipLaunchKernelGGL(merge_kernel, dim3((unsigned)num_q_heads, (unsigned)batch), dim3(kHeadDim), 0,
