@@ -326,7 +326,7 @@ __global__ __launch_bounds__(256, 2) void partition_kernel(Params p) {
 // partial (empty ones: m = kNegBig, l = 0), so all loads are issued at once with no
 // dependency on the row's length; empty partials are selected away, never multiplied.
 __global__ __launch_bounds__(kHeadDim) void merge_kernel(Params p) {
-  constexpr int kBatch = 8;
+  constexpr int kBatch = 16;  // partials loaded per round (one round for up to 16 partitions)
   const int h = blockIdx.x;
   const int b = blockIdx.y;
   const int d = threadIdx.x;
@@ -337,9 +337,10 @@ __global__ __launch_bounds__(kHeadDim) void merge_kernel(Params p) {
 #pragma unroll
     for (int k = 0; k < kBatch; ++k) {
       const int s = s0 + k < p.max_splits ? s0 + k : p.max_splits - 1;
-      m[k] = p.part_ml[(slot0 + s) * 2];
-      l[k] = p.part_ml[(slot0 + s) * 2 + 1];
-      o[k] = p.part_o[(slot0 + s) * kHeadDim + d];
+      // read once: non-temporal
+      m[k] = __builtin_nontemporal_load(p.part_ml + (slot0 + s) * 2);
+      l[k] = __builtin_nontemporal_load(p.part_ml + (slot0 + s) * 2 + 1);
+      o[k] = __builtin_nontemporal_load(p.part_o + (slot0 + s) * kHeadDim + d);
     }
 #pragma unroll
     for (int k = 0; k < kBatch; ++k) {

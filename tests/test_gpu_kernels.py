@@ -284,6 +284,28 @@ def test_paged_decode_batch32_ragged_full_size(hip):
         assert _maxabs(one[0], out[r]) <= ATOL
 
 
+def test_paged_decode_workspace_reused_across_shapes(hip):
+    # One workspace serves calls of different batch, lengths and split counts in a row
+    # (partials of earlier calls left in it must not leak into later results).
+    banner("paged decode: one workspace, several call shapes")
+    from fast_infer_amd import paged_attention, paged_attention_workspace
+
+    ws = paged_attention_workspace(32, 24, 8, 4096, 128, DEV)
+    q, kc, vc, table = _big_decode_inputs(32, [4096] * 32, 2048, 5)
+    calls = [(32, [4096] * 32), (4, [3000, 17, 4096, 1]), (32, [600 + 100 * i for i in range(32)]),
+             (9, [0, 513, 4096, 2048, 1, 64, 65, 999, 4000]), (32, [4096] * 32)]
+    for rep, (B, lens) in enumerate(calls):
+        cl = torch.tensor(lens, dtype=torch.int32, device=DEV)
+        out = paged_attention(q[:B], kc, vc, table[:B].to(DEV), 64, 4096, context_lens=cl,
+                              workspace=ws)
+        torch.cuda.synchronize()
+        rows = sorted({0, B // 2, B - 1})
+        sub = torch.tensor(rows)
+        ref = OA.paged_attention(q.cpu()[sub], kc.cpu(), vc.cpu(), table[sub], 64,
+                                 [lens[r] for r in rows])
+        assert _maxabs(out.cpu()[sub], ref) <= ATOL, (rep, B)
+
+
 # --------------------------------------------------------------------------- prefill
 
 
