@@ -11,6 +11,8 @@ serve them.  The same line carries:
 
 * ``prefill`` — causal prefill batch 4 x seq 4096 with the K/V pool write, TFLOP/s;
 * ``decode_b1_ctx256`` / ``prefill_b1_s512`` — the small configurations (latency);
+* ``rope_store_kv`` — the fused RoPE + K/V pool write (batch 4 x 4096 prefill, batch 64
+  decode), GB/s of algorithmic traffic;
 * ``decode_28layer_b64`` — a 28-layer decode step over per-layer pools, batch 64,
   lognormal contexts (median 1024, sigma 0.5, clipped to [64, 4096]): step latency
   and decode tokens/s;
@@ -46,7 +48,7 @@ def _args():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", default="", help="comma list: decode,prefill,small,e2e")
+    ap.add_argument("--only", default="", help="comma list: decode,prefill,small,e2e,rope")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device copy (reference for PMC byte counters)")
     return ap.parse_args()
@@ -201,6 +203,32 @@ def bench_decode_28layer(torch, fi, timer, steps, warmup, dev):
     return dict(t=t, bytes=nbytes, gbs=nbytes / t / 1e9, tok_s=B / t, lens=lens)
 
 
+def bench_rope(torch, fi, timer, steps, warmup, dev, B, T, start, pool_blocks, return_k):
+    """Fused RoPE + pool write on q/k/v views of one projection output (model.py:88-101)."""
+    from fast_infer_amd import roofline as R
+
+    g = torch.Generator(device=dev).manual_seed(7)
+    qkv = torch.randn(B, T, (HQ + 2 * HKV) * D, device=dev, generator=g, dtype=torch.float16)
+    q, k, v = qkv.split([HQ * D, HKV * D, HKV * D], dim=-1)
+    q, k, v = q.view(B, T, HQ, D), k.view(B, T, HKV, D), v.view(B, T, HKV, D)
+    cos, sin = fi.precompute_freqs(D, 4096, device=dev)
+    cos, sin = cos.half(), sin.half()
+    kc = torch.zeros(pool_blocks, BS, HKV, D, device=dev, dtype=torch.float16)
+    vc = torch.zeros_like(kc)
+    per_row = pool_blocks // B
+    table = torch.randperm(pool_blocks, generator=torch.Generator().manual_seed(7)).int()
+    table = table.view(B, per_row).to(dev)
+    q_out = torch.empty(B, T, HQ, D, device=dev, dtype=torch.float16)
+
+    def step():
+        fi.rope_store_kv(q, k, v, cos, sin, start, kc, vc, table, return_k=return_k,
+                         q_out=q_out)
+
+    t = timer.run(step, steps, warmup)
+    nbytes = R.rope_store_bytes(B, T, HQ, HKV, D, T, True, return_k)
+    return dict(t=t, bytes=nbytes, gbs=nbytes / t / 1e9)
+
+
 # ----------------------------------------------------------------------------- CPU
 
 
@@ -276,7 +304,7 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     timer = Timer(torch)
-    only = set(filter(None, a.only.split(","))) or {"decode", "prefill", "small", "e2e"}
+    only = set(filter(None, a.only.split(","))) or {"decode", "prefill", "small", "e2e", "rope"}
     cores = _cores()
     steps, warm = a.steps, a.warmup
     out = {"metric": METRIC}
@@ -348,6 +376,23 @@ def main():
             "context_tokens": sum(e["lens"]), "lognormal_sigma": 0.5}
         print(f"[bench] 28-layer b64 step: {e['t'] * 1e3:.3f} ms, {e['gbs']:.0f} GB/s",
               file=sys.stderr, flush=True)
+
+    if "rope" in only:
+        rp = bench_rope(torch, fi, timer, steps, warm, dev, 4, 4096, 0, 256, True)
+        rd = bench_rope(torch, fi, timer, steps, warm, dev, 64, 1, 1000, 1024, False)
+        out["rope_store_kv"] = {
+            "workload": "fused RoPE + K/V pool write on strided q/k/v views, batch 4 x 4096 "
+                        "tokens (prefill, rotated k returned) and batch 64 x 1 token at "
+                        "position 1000 (decode); 24 q / 8 kv heads, block_size 64",
+            "prefill_b4_s4096": {"us_per_call": round(rp["t"] * 1e6, 2),
+                                 "GB/s": round(rp["gbs"], 1),
+                                 "frac_hbm": round(rp["gbs"] / R.HBM_PEAK_GBS, 4),
+                                 "algorithmic_bytes": rp["bytes"],
+                                 "traffic": _traffic("rope_b4_s4096")},
+            "decode_b64": {"us_per_call": round(rd["t"] * 1e6, 2), "GB/s": round(rd["gbs"], 1),
+                           "algorithmic_bytes": rd["bytes"]}}
+        print(f"[bench] rope+store b4 s4096: {rp['t'] * 1e6:.1f} us, {rp['gbs']:.0f} GB/s; "
+              f"decode b64 {rd['t'] * 1e6:.2f} us", file=sys.stderr, flush=True)
 
     if not a.no_cpu_baseline:
         if dec is not None:

@@ -1,14 +1,18 @@
 """fast_infer_amd — MI355X-native attention hot path of Fast_Infer.
 
 Drop-in replacements for the reference's ``kernels/attention.py`` (``flash_attention``,
-``paged_attention``) and ``kv_cache.py`` (``KVCache``), plus the K/V pool writes of
-``model.py`` (``store_kv_prefill`` / ``store_kv_decode``), all running hand-written
-gfx950 HIP kernels through the C ABI of ``include/fast_infer_amd.h``.
+``paged_attention``), ``kv_cache.py`` (``KVCache``) and ``kernels/rope.py``
+(``apply_rope``, fused with the pool write in ``rope_store_kv``), plus the K/V pool
+writes of ``model.py`` (``store_kv_prefill`` / ``store_kv_decode``), all running
+hand-written gfx950 HIP kernels through the C ABI of ``include/fast_infer_amd.h``.
 """
 
 from .attention import flash_attention, paged_attention, paged_attention_workspace
 from .kv_cache import KVCache
-from .kv_store import allocate_prefill, store_kv, store_kv_decode, store_kv_prefill
+from .kv_store import (allocate_decode, allocate_prefill, store_kv, store_kv_decode,
+                       store_kv_prefill)
+from .rope import (apply_rope, precompute_freqs, rope_store_kv, rope_store_kv_decode,
+                   rope_store_kv_prefill)
 
 __all__ = [
     "flash_attention",
@@ -19,4 +23,10 @@ __all__ = [
     "store_kv_prefill",
     "store_kv_decode",
     "allocate_prefill",
+    "allocate_decode",
+    "apply_rope",
+    "precompute_freqs",
+    "rope_store_kv",
+    "rope_store_kv_prefill",
+    "rope_store_kv_decode",
 ]

@@ -69,6 +69,20 @@ SIGNATURES = {
          _i64, _i64, _i64, _ptr,
          _ptr],
     ),
+    "fi_rope_store_kv": (
+        ctypes.c_int,
+        [_ptr, _i64, _i64, _i64,                 # q, strides
+         _ptr, _i64, _i64, _i64,                 # k, strides
+         _ptr, _i64, _i64, _i64,                 # v, strides
+         _ptr, _ptr, _i64,                       # cos, sin, table rows
+         _ptr, _i64, _i64, _i64,                 # q_out, strides
+         _ptr, _i64, _i64, _i64,                 # k_out, strides
+         _ptr, _ptr, _i64, _i64,                 # pools, N, block_size
+         _ptr, _i64, _i64,                       # block table, stride, max blocks
+         _i64, _i64, _i64, _i64, _i64,           # batch, tokens, Hq, Hkv, D
+         _i64, _ptr,                             # start_pos, start_pos_per_seq
+         _ptr],                                  # stream
+    ),
     "fi_selftest_mfma_f16": (ctypes.c_int, [_ptr, _ptr, _ptr, _ptr]),
 }
 
@@ -107,6 +121,13 @@ def check(rc: int, what: str) -> None:
         raise FastInferError(f"{what} failed ({_ERROR_NAMES.get(rc, rc)}): {msg}")
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_handle(device: torch.device) -> int:
-    """hipStream_t of torch's current stream on `device`."""
+    """hipStream_t of torch's current stream on `device` (the raw-handle query skips
+    building a Stream object: a few microseconds per call on the decode path)."""
+    if _raw_stream is not None:
+        index = device.index if device.index is not None else torch.cuda.current_device()
+        return _raw_stream(index)
     return torch.cuda.current_stream(device).cuda_stream

@@ -101,12 +101,17 @@ def store_kv_decode(kv_cache, layer_idx: int, k: torch.Tensor, v: torch.Tensor,
     allocates lazily; copies row b to block ``block_table[b, pos // bs]``, slot
     ``pos % bs``."""
     batch_size = k.shape[0]
-    block_idx = token_pos // kv_cache.block_size
     if layer_idx == 0:
         kv_cache.num_tokens += 1
+    allocate_decode(kv_cache, batch_size, token_pos)
+    store_kv(k.unsqueeze(1), v.unsqueeze(1), kv_cache.k[layer_idx], kv_cache.v[layer_idx],
+             kv_cache.block_table, token_pos)
+
+
+def allocate_decode(kv_cache, batch_size: int, token_pos: int) -> None:
+    """Allocation loop of model.py:196-198: every row gets blocks up to token_pos's."""
+    block_idx = token_pos // kv_cache.block_size
     kv_cache._grow_batch(batch_size)
     for b in range(batch_size):
         while kv_cache.allocated_blocks(b) <= block_idx:
             kv_cache.alloc_block(b)
-    store_kv(k.unsqueeze(1), v.unsqueeze(1), kv_cache.k[layer_idx], kv_cache.v[layer_idx],
-             kv_cache.block_table, token_pos)

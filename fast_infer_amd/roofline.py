@@ -6,7 +6,10 @@ what the algorithm must move or compute, independent of how a kernel does it:
 * paged decode — every context token's K and V row of every kv head once (4 KiB per
   token at 8 kv heads x 128 dims x fp16 x 2), plus q and o, plus the block-table
   entries covering the context;
-* causal prefill — 4 * B * H * S^2 * D / 2 flops (QK^T and PV over the causal half).
+* causal prefill — 4 * B * H * S^2 * D / 2 flops (QK^T and PV over the causal half);
+* fused RoPE + KV write — q, k, v rows read once, the cos/sin rows of the distinct
+  positions read once, rotated q (and k when returned) written once, k and v rows
+  written into the pool once.
 """
 
 from __future__ import annotations
@@ -35,3 +38,16 @@ def prefill_flops(batch: int, num_heads: int, seq_len: int, head_dim: int) -> fl
 def prefill_scatter_bytes(batch: int, seq_len: int, num_kv_heads: int, head_dim: int) -> int:
     """Bytes the fused K/V pool write stores (K and V rows of every token)."""
     return batch * seq_len * num_kv_heads * head_dim * 2 * 2
+
+
+def rope_store_bytes(batch: int, tokens: int, num_q_heads: int, num_kv_heads: int,
+                     head_dim: int, positions: int, pool: bool, return_k: bool) -> int:
+    """Algorithmic HBM bytes of one fused RoPE (+ pool write) call; ``positions`` is the
+    number of distinct table rows the call touches."""
+    row = head_dim * 2
+    n = batch * tokens
+    read = n * (num_q_heads + num_kv_heads + (num_kv_heads if pool else 0)) * row
+    read += positions * row * 2
+    write = n * num_q_heads * row
+    write += n * num_kv_heads * row * ((1 if return_k else 0) + (2 if pool else 0))
+    return read + write

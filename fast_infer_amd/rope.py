@@ -1,0 +1,177 @@
+"""Rotary position embedding (kernels/rope.py) on the gfx950 kernel, optionally fused
+with the paged K/V write of model.py:117 / :120.
+
+``precompute_freqs`` and ``apply_rope`` keep the reference's names and signatures
+(kernels/rope.py:9-16, :26-44).  ``apply_rope`` is bit-exact with the reference's fp16
+tensor arithmetic.  ``rope_store_kv`` is the fused form: it rotates q and k at table
+rows ``start + t`` and, given a pool, writes rotated k and v into it in the same pass
+(replacing ``apply_rope`` followed by ``store_kv``); ``rope_store_kv_prefill`` /
+``rope_store_kv_decode`` apply it to a ``KVCache`` with the model's allocation steps.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .kv_store import allocate_decode, allocate_prefill
+
+
+def precompute_freqs(head_dim: int, max_seq_len: int, theta: float = 500000.0,
+                     device: torch.device | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """cos and sin tables ``[max_seq_len, head_dim]`` (fp32) as kernels/rope.py:9-16
+    builds them: angle(p, i) = p / theta^(2(i mod head_dim/2)/head_dim), the half-width
+    frequency vector repeated twice.  Table setup, not the hot path."""
+    freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2, device=device).float() / head_dim))
+    positions = torch.arange(max_seq_len, device=device).float()
+    angles = torch.outer(positions, freq)
+    angles = torch.cat([angles, angles], dim=-1)
+    return angles.cos(), angles.sin()
+
+
+def _check_rows(name: str, t: torch.Tensor, heads: int | None = None) -> None:
+    if t.dtype != torch.float16:
+        raise TypeError(f"{name} must be float16, got {t.dtype}")
+    if t.device.type != "cuda":
+        raise RuntimeError(f"{name} must be on a HIP device; fast_infer_amd has no CPU path")
+    if t.dim() != 4 or t.shape[-1] != 128:
+        raise ValueError(f"{name} must be [batch, tokens, heads, 128], got {tuple(t.shape)}")
+    if heads is not None and t.shape[2] != heads:
+        raise ValueError(f"{name} has {t.shape[2]} heads, expected {heads}")
+
+
+def _rows(t: torch.Tensor) -> torch.Tensor:
+    if t.stride(-1) != 1 or any(s % 8 for s in t.stride()[:-1]) or t.data_ptr() % 16:
+        return t.contiguous()
+    return t
+
+
+def _table(name: str, t: torch.Tensor, device) -> torch.Tensor:
+    if t.dim() != 2 or t.shape[1] != 128:
+        raise ValueError(f"{name} must be [rows, 128], got {tuple(t.shape)}")
+    if t.dtype != torch.float16 or t.device != device:
+        t = t.to(device=device, dtype=torch.float16)
+    return t if t.is_contiguous() and t.data_ptr() % 16 == 0 else t.contiguous()
+
+
+def rope_store_kv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor | None,
+                  cos_table: torch.Tensor, sin_table: torch.Tensor, start_pos: int = 0,
+                  k_cache: torch.Tensor | None = None, v_cache: torch.Tensor | None = None,
+                  block_table: torch.Tensor | None = None, *,
+                  start_positions: torch.Tensor | None = None, return_k: bool = True,
+                  q_out: torch.Tensor | None = None
+                  ) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """Rotate q ``[B, T, Hq, 128]`` and k ``[B, T, Hkv, 128]`` at table rows
+    ``start + t`` (``start`` = ``start_positions[b]`` if given, else ``start_pos``), with
+    fp16 tables ``cos_table`` / ``sin_table`` ``[rows, 128]`` (fp32 tables are converted
+    on every call; pass fp16 ones on the hot path).  With a pool, rotated k and v also go
+    to ``block_table[b, pos // bs]``, slot ``pos % bs`` (block-table entries past the
+    table or outside the pool are skipped).  Positions outside the table are an error for
+    a scalar ``start_pos`` (the reference's table indexing fails there); with
+    ``start_positions`` such tokens are skipped on the device, their q/k rows left
+    unwritten.  Returns (q_rot, k_rot or None)."""
+    _check_rows("q", q)
+    batch, tokens, num_q_heads, _ = q.shape
+    _check_rows("k", k)
+    num_kv_heads = k.shape[2]
+    if k.shape[:2] != q.shape[:2]:
+        raise ValueError(f"k {tuple(k.shape)} does not match q {tuple(q.shape)}")
+    pool = k_cache is not None
+    if pool:
+        if v is None or v_cache is None or block_table is None:
+            raise ValueError("the pool write needs v, v_cache and block_table")
+        _check_rows("v", v, num_kv_heads)
+        if v.shape[:2] != q.shape[:2]:
+            raise ValueError(f"v {tuple(v.shape)} does not match q {tuple(q.shape)}")
+        for name, t in (("k_cache", k_cache), ("v_cache", v_cache)):
+            if t.dtype != torch.float16 or t.device.type != "cuda":
+                raise TypeError(f"{name} must be a float16 HIP tensor")
+        if (k_cache.dim() != 4 or v_cache.shape != k_cache.shape
+                or k_cache.shape[2] != num_kv_heads or k_cache.shape[3] != 128):
+            raise ValueError(f"pool {tuple(k_cache.shape)} does not match k {tuple(k.shape)}")
+        if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+            raise ValueError("pools must be contiguous")
+        if block_table.dtype != torch.int32 or block_table.dim() != 2:
+            raise TypeError("block_table must be a 2-D int32 tensor")
+        if block_table.shape[0] < batch:
+            raise ValueError("block_table has fewer rows than the batch")
+        if block_table.stride(-1) != 1:
+            block_table = block_table.contiguous()
+    cos_t = _table("cos_table", cos_table, q.device)
+    sin_t = _table("sin_table", sin_table, q.device)
+    if cos_t.shape != sin_t.shape:
+        raise ValueError("cos and sin tables differ in shape")
+    if start_positions is not None:
+        start_positions = start_positions.to(device=q.device, dtype=torch.int32).contiguous()
+        if start_positions.numel() < batch:
+            raise ValueError("start_positions has fewer entries than the batch")
+    elif tokens > 0 and (start_pos < 0 or start_pos + tokens > cos_t.shape[0]):
+        raise IndexError(f"positions {start_pos}..{start_pos + tokens - 1} outside the "
+                         f"{cos_t.shape[0]}-row table")
+    if q_out is None:
+        q_out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    elif q_out.shape != q.shape:
+        raise ValueError("q_out must have q's shape")
+    k_out = torch.empty(k.shape, dtype=k.dtype, device=k.device) if return_k else None
+    if batch == 0 or tokens == 0:
+        return q_out, k_out
+    q, k = _rows(q), _rows(k)
+    v = _rows(v) if v is not None else None
+    lib = _lib.load()
+    rc = lib.fi_rope_store_kv(
+        q.data_ptr(), q.stride(0), q.stride(1), q.stride(2),
+        k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
+        v.data_ptr() if v is not None else None,
+        *(v.stride()[:3] if v is not None else (0, 0, 0)),
+        cos_t.data_ptr(), sin_t.data_ptr(), cos_t.shape[0],
+        q_out.data_ptr(), q_out.stride(0), q_out.stride(1), q_out.stride(2),
+        k_out.data_ptr() if k_out is not None else None,
+        *(k_out.stride()[:3] if k_out is not None else (0, 0, 0)),
+        k_cache.data_ptr() if pool else None, v_cache.data_ptr() if pool else None,
+        k_cache.shape[0] if pool else 0, k_cache.shape[1] if pool else 0,
+        block_table.data_ptr() if pool else None,
+        block_table.stride(0) if pool else 0, block_table.shape[1] if pool else 0,
+        batch, tokens, num_q_heads, num_kv_heads, 128,
+        int(start_pos), None if start_positions is None else start_positions.data_ptr(),
+        _lib.stream_handle(q.device))
+    _lib.check(rc, "rope_store_kv")
+    return q_out, k_out
+
+
+def apply_rope(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor,
+               sin: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """kernels/rope.py:26-44: q ``[B, S, Hq, 128]``, k ``[B, S, Hkv, 128]`` fp16 (strided
+    views fine), cos/sin ``[S, 128]`` fp16 (the table rows of the S positions).
+    Returns rotated (q, k), bit-exact with the reference."""
+    if cos.dim() != 2 or cos.shape[0] != q.shape[1]:
+        raise ValueError(f"cos must be [seq_len, head_dim] for seq_len {q.shape[1]}")
+    return rope_store_kv(q, k, None, cos, sin, 0)
+
+
+def rope_store_kv_prefill(kv_cache, layer_idx: int, q: torch.Tensor, k: torch.Tensor,
+                          v: torch.Tensor, cos_table: torch.Tensor, sin_table: torch.Tensor,
+                          return_k: bool = True):
+    """model.py:101 + :117 (:162-183) in one pass: positions 0..S-1; at layer 0 sets
+    ``num_tokens = S``; allocates each row's blocks; returns (q_rot, k_rot)."""
+    batch_size, seq_len = q.shape[0], q.shape[1]
+    if layer_idx == 0:
+        kv_cache.num_tokens = seq_len
+    allocate_prefill(kv_cache, batch_size, seq_len)
+    return rope_store_kv(q, k, v, cos_table, sin_table, 0, kv_cache.k[layer_idx],
+                         kv_cache.v[layer_idx], kv_cache.block_table, return_k=return_k)
+
+
+def rope_store_kv_decode(kv_cache, layer_idx: int, q: torch.Tensor, k: torch.Tensor,
+                         v: torch.Tensor, cos_table: torch.Tensor, sin_table: torch.Tensor,
+                         token_pos: int) -> torch.Tensor:
+    """model.py:101 + :120 (:185-201) in one pass for one token per row at position
+    ``token_pos``: q ``[B, Hq, 128]``, k/v ``[B, Hkv, 128]``.  At layer 0 increments
+    ``num_tokens``; allocates lazily; returns q_rot ``[B, Hq, 128]``."""
+    batch_size = q.shape[0]
+    if layer_idx == 0:
+        kv_cache.num_tokens += 1
+    allocate_decode(kv_cache, batch_size, token_pos)
+    q_rot, _ = rope_store_kv(q.unsqueeze(1), k.unsqueeze(1), v.unsqueeze(1), cos_table,
+                             sin_table, token_pos, kv_cache.k[layer_idx], kv_cache.v[layer_idx],
+                             kv_cache.block_table, return_k=False)
+    return q_rot.squeeze(1)

@@ -154,6 +154,45 @@ FI_API int fi_kv_store(const void* k, int64_t k_sb, int64_t k_st, int64_t k_sh,
                 void* stream);
 
 /*
+ * Rotary position embedding, optionally fused with the paged K/V write.
+ * Replaces apply_rope(q, k, cos, sin) at kernels/rope.py:26-44 (call site model.py:101)
+ * and, with a pool, the K/V stores after it (model.py:117 -> :162-183, model.py:120 ->
+ * :185-201).
+ *
+ *   q, q_out : [batch, num_tokens, num_q_heads, head_dim], strides (q_sb, q_st, q_sh) /
+ *              (qo_sb, qo_st, qo_sh); q_out may be q itself (same strides).
+ *   k, v     : [batch, num_tokens, num_kv_heads, head_dim], strides (k_*, v_*).
+ *   cos/sin  : fp16 [table_rows, head_dim] dense, the rows of the reference's tables
+ *              (kernels/rope.py:9-16, cast to fp16 at model.py:75-76).
+ *   Token t of row b uses table row pos = start + t, start = start_pos_per_seq[b] if
+ *   that pointer is non-null, else start_pos.  Each element is
+ *   fp16(fp16(x * cos) + fp16(rotate_half(x) * sin)) with rotate_half(x)[i] = -x[i+64]
+ *   (i < 64) and x[i-64] (i >= 64): bit-exact with the reference's fp16 tensor ops.
+ *   A token whose pos is outside [0, table_rows) is skipped entirely (q_out/k_out rows
+ *   left unwritten, nothing written to the pool).
+ *   k_out (optional, may be NULL): rotated k, strides (ko_sb, ko_st, ko_sh).
+ *   k_cache (optional, may be NULL): rotated k and the unrotated v are also written to
+ *   k_cache / v_cache [num_pool_blocks, block_size, num_kv_heads, head_dim] at block
+ *   block_table[b, pos / block_size], slot pos % block_size; positions whose logical
+ *   block is >= max_blocks_per_seq or whose entry is outside [0, num_pool_blocks) are
+ *   skipped (as fi_kv_store).
+ *   Rows must be 16-byte aligned (pointers 16-byte aligned, strides multiples of 8).
+ */
+FI_API int fi_rope_store_kv(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh,
+                     const void* k, int64_t k_sb, int64_t k_st, int64_t k_sh,
+                     const void* v, int64_t v_sb, int64_t v_st, int64_t v_sh,
+                     const void* cos_table, const void* sin_table, int64_t table_rows,
+                     void* q_out, int64_t qo_sb, int64_t qo_st, int64_t qo_sh,
+                     void* k_out, int64_t ko_sb, int64_t ko_st, int64_t ko_sh,
+                     void* k_cache, void* v_cache, int64_t num_pool_blocks,
+                     int64_t block_size, const int32_t* block_table, int64_t bt_stride,
+                     int64_t max_blocks_per_seq,
+                     int64_t batch, int64_t num_tokens, int64_t num_q_heads,
+                     int64_t num_kv_heads, int64_t head_dim,
+                     int64_t start_pos, const int32_t* start_pos_per_seq,
+                     void* stream);
+
+/*
  * Self-test of the gfx950 MFMA fragment layout the attention kernels assume
  * (no counterpart in the reference; used by the test suite).  One wave computes
  * C[16x16] = A[16x32] * B[32x16] with v_mfma_f32_16x16x32_f16, where lane l holds

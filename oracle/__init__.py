@@ -1,4 +1,4 @@
-"""CPU oracle for the attention hot path — TEST INFRASTRUCTURE, never a product path.
+"""CPU oracle for the attention hot path and its RoPE producer — TEST INFRASTRUCTURE, never a product path.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may
 import, call, link or execute anything in this package, and only as the checker (or
@@ -12,6 +12,9 @@ Contents (each function cites the reference file:line it restates):
   outputs.
 * ``kv`` — pure-Python restatement of the KV pool writes (model.py:162-201,
   kv_cache.py:69-103) and of the block allocator (kv_cache.py:12-113).
+* ``rope`` — numpy restatement of the RoPE table and of its fp16 application
+  (kernels/rope.py:9-44), and of RoPE followed by the pool write (model.py:101,
+  :117, :120).
 * ``ref_algo.c`` (+ ``native``) — the same tile algorithms in C with OpenMP, used
   as the CPU baseline ("port").
 

@@ -33,6 +33,7 @@ def lib():
 def test_header_declares_entry_points():
     names = _declared()
     for n in ("fi_flash_attention_fwd", "fi_paged_attention_fwd", "fi_kv_store",
+              "fi_rope_store_kv",
               "fi_paged_attention_workspace_size", "fi_last_error", "fi_version"):
         assert n in names
 
@@ -102,6 +103,34 @@ def test_empty_calls_are_noops(lib):
                                       1.0, None, None, 0, 64, None, 0, 0, None) == _lib.FI_OK
     assert lib.fi_kv_store(None, 8, 8, 8, None, 8, 8, 8, None, None, 1, 64, 1, 128, None, 1,
                            1, 0, 5, 0, None, None) == _lib.FI_OK
+
+
+def _rope_args(**kw):
+    """fi_rope_store_kv's 38 arguments, all valid and 16-byte aligned, with overrides."""
+    a = dict(q=16, q_sb=8, q_st=8, q_sh=8, k=16, k_sb=8, k_st=8, k_sh=8, v=16, v_sb=8, v_st=8,
+             v_sh=8, cos=16, sin=16, rows=64, q_out=16, qo_sb=8, qo_st=8, qo_sh=8, k_out=16,
+             ko_sb=8, ko_st=8, ko_sh=8, k_cache=16, v_cache=16, pool_blocks=4, block_size=64,
+             table=16, bt_stride=4, max_blocks=4, batch=1, tokens=1, hq=8, hkv=8, head_dim=128,
+             start=0, starts=None, stream=None)
+    a.update(kw)
+    return list(a.values())
+
+
+def test_rope_store_kv_validation(lib):
+    from fast_infer_amd import _lib
+
+    assert lib.fi_rope_store_kv(*_rope_args(head_dim=64)) == _lib.FI_ERR_UNSUPPORTED
+    assert b"head_dim 64" in lib.fi_last_error()
+    assert lib.fi_rope_store_kv(*_rope_args(q=18)) == _lib.FI_ERR_INVALID
+    assert b"aligned" in lib.fi_last_error()
+    assert lib.fi_rope_store_kv(*_rope_args(k_st=12)) == _lib.FI_ERR_INVALID
+    assert lib.fi_rope_store_kv(*_rope_args(v=None)) == _lib.FI_ERR_INVALID
+    assert b"null" in lib.fi_last_error()
+    assert lib.fi_rope_store_kv(*_rope_args(block_size=0)) == _lib.FI_ERR_INVALID
+    assert lib.fi_rope_store_kv(*_rope_args(tokens=-1)) == _lib.FI_ERR_INVALID
+    # empty calls return before touching any pointer
+    assert lib.fi_rope_store_kv(*_rope_args(batch=0, q=None, k=None)) == _lib.FI_OK
+    assert lib.fi_rope_store_kv(*_rope_args(tokens=0)) == _lib.FI_OK
 
 
 def test_workspace_size(lib):
