@@ -11,6 +11,8 @@ serve them.  The same line carries:
 
 * ``prefill`` — causal prefill batch 4 x seq 4096 with the K/V pool write, TFLOP/s;
 * ``decode_b1_ctx256`` / ``prefill_b1_s512`` — the small configurations (latency);
+* ``decode_step_28layer_b64_paged`` — the same step with the device block manager (one
+  append per step) and the fused RoPE + pool write per layer before attention;
 * ``rope_store_kv`` — the fused RoPE + K/V pool write (batch 4 x 4096 prefill, batch 64
   decode), GB/s of algorithmic traffic;
 * ``decode_28layer_b64`` — a 28-layer decode step over per-layer pools, batch 64,
@@ -229,6 +231,53 @@ def bench_rope(torch, fi, timer, steps, warmup, dev, B, T, start, pool_blocks, r
     return dict(t=t, bytes=nbytes, gbs=nbytes / t / 1e9)
 
 
+def bench_decode_step_paged(torch, fi, timer, steps, warmup, dev):
+    """A 28-layer decode step as a serving loop runs it with the device block manager:
+    one append of a token to every row, then per layer the fused RoPE + pool write at the
+    rows' own positions and paged attention over the rows' own lengths.  Batch 64,
+    lognormal contexts (median 1024, sigma 0.5, clipped to [64, 4096])."""
+    from fast_infer_amd import roofline as R
+
+    L, B = 28, 64
+    gen = torch.Generator().manual_seed(4)
+    lens = torch.exp(torch.randn(B, generator=gen) * 0.5 + math.log(1024)).round()
+    lens = lens.clamp(64, 4096).int()
+    extra = steps + warmup + 1
+    max_len = 4096 + extra
+    N = int(sum(math.ceil((int(n) + extra) / BS) for n in lens)) + B
+    cache = fi.PagedKVCache(L, HKV, D, max_len, BS, dev, max_batch=B, num_blocks=N)
+    g = torch.Generator(device=dev).manual_seed(4)
+    cache.k.normal_(generator=g)
+    cache.v.normal_(generator=g)
+    cache.append(lens.to(dev))
+    cache.check()
+    cos, sin = fi.precompute_freqs(D, max_len, device=dev)
+    cos, sin = cos.half(), sin.half()
+    qkv = torch.randn(L, B, 1, (HQ + 2 * HKV) * D, device=dev, generator=g, dtype=torch.float16)
+    q = qkv[..., :HQ * D].view(L, B, 1, HQ, D)
+    k = qkv[..., HQ * D:(HQ + HKV) * D].view(L, B, 1, HKV, D)
+    v = qkv[..., (HQ + HKV) * D:].view(L, B, 1, HKV, D)
+    q_rot = torch.empty(B, 1, HQ, D, device=dev, dtype=torch.float16)
+    ws = fi.paged_attention_workspace(B, HQ, HKV, max_len, D, dev)
+
+    def step():
+        starts, ctx = cache.append(1)
+        for layer in range(L):
+            fi.rope_store_kv(q[layer], k[layer], v[layer], cos, sin, 0, cache.k[layer],
+                             cache.v[layer], cache.block_table, start_positions=starts,
+                             return_k=False, q_out=q_rot)
+            fi.paged_attention(q_rot[:, 0], cache.k[layer], cache.v[layer], cache.block_table,
+                               BS, max_len, context_lens=ctx, workspace=ws)
+
+    n_steps, n_warm = max(1, steps // 10), max(1, warmup // 5)
+    t = timer.run(step, n_steps, n_warm)
+    cache.check()
+    mid = [int(n) + n_warm + n_steps // 2 + 1 for n in lens]
+    nbytes = L * (R.decode_bytes(mid, HQ, HKV, D, BS)
+                  + R.rope_store_bytes(B, 1, HQ, HKV, D, B, True, False))
+    return dict(t=t, bytes=nbytes, gbs=nbytes / t / 1e9, tok_s=B / t, tokens=sum(mid))
+
+
 # ----------------------------------------------------------------------------- CPU
 
 
@@ -376,6 +425,17 @@ def main():
             "context_tokens": sum(e["lens"]), "lognormal_sigma": 0.5}
         print(f"[bench] 28-layer b64 step: {e['t'] * 1e3:.3f} ms, {e['gbs']:.0f} GB/s",
               file=sys.stderr, flush=True)
+        del e
+        f = bench_decode_step_paged(torch, fi, timer, steps, warm, dev)
+        out["decode_step_28layer_b64_paged"] = {
+            "workload": "28-layer decode step with the device block manager: append one token "
+                        "per row, then per layer fused RoPE + pool write and paged attention "
+                        "over per-row lengths; batch 64, lognormal contexts as above",
+            "step_ms": round(f["t"] * 1e3, 4), "tokens_per_s": round(f["tok_s"], 1),
+            "GB/s": round(f["gbs"], 1), "frac_hbm": round(f["gbs"] / R.HBM_PEAK_GBS, 4),
+            "context_tokens": f["tokens"]}
+        print(f"[bench] 28-layer b64 paged step (append + rope + attention): "
+              f"{f['t'] * 1e3:.3f} ms, {f['gbs']:.0f} GB/s", file=sys.stderr, flush=True)
 
     if "rope" in only:
         rp = bench_rope(torch, fi, timer, steps, warm, dev, 4, 4096, 0, 256, True)

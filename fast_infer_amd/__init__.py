@@ -3,7 +3,8 @@
 Drop-in replacements for the reference's ``kernels/attention.py`` (``flash_attention``,
 ``paged_attention``), ``kv_cache.py`` (``KVCache``) and ``kernels/rope.py``
 (``apply_rope``, fused with the pool write in ``rope_store_kv``), plus the K/V pool
-writes of ``model.py`` (``store_kv_prefill`` / ``store_kv_decode``), all running
+writes of ``model.py`` (``store_kv_prefill`` / ``store_kv_decode``) and a device-resident
+block allocator with per-sequence lengths (``PagedKVCache``), all running
 hand-written gfx950 HIP kernels through the C ABI of ``include/fast_infer_amd.h``.
 """
 
@@ -11,6 +12,7 @@ from .attention import flash_attention, paged_attention, paged_attention_workspa
 from .kv_cache import KVCache
 from .kv_store import (allocate_decode, allocate_prefill, store_kv, store_kv_decode,
                        store_kv_prefill)
+from .paged_cache import PagedKVCache
 from .rope import (apply_rope, precompute_freqs, rope_store_kv, rope_store_kv_decode,
                    rope_store_kv_prefill)
 
@@ -19,6 +21,7 @@ __all__ = [
     "paged_attention",
     "paged_attention_workspace",
     "KVCache",
+    "PagedKVCache",
     "store_kv",
     "store_kv_prefill",
     "store_kv_decode",

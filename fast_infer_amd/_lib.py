@@ -83,8 +83,31 @@ SIGNATURES = {
          _i64, _ptr,                             # start_pos, start_pos_per_seq
          _ptr],                                  # stream
     ),
+    "fi_kv_append": (
+        ctypes.c_int,
+        [_ptr, _i64, _i64,                       # block table, stride, max blocks
+         _ptr, _ptr, _ptr, _ptr,                 # num_alloc, seq_lens, free_queue, state
+         _i64, _i64, _i64,                       # num_blocks, block_size, batch
+         _ptr, _i64,                             # num_new (per row), num_new_all
+         _ptr, _ptr,                             # start_pos_out, context_lens_out
+         _ptr],                                  # stream
+    ),
+    "fi_kv_release": (
+        ctypes.c_int,
+        [_ptr, _i64, _i64, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _ptr, _ptr],
+    ),
+    "fi_kv_reset": (
+        ctypes.c_int,
+        [_ptr, _i64, _i64, _i64, _ptr, _ptr, _ptr, _ptr, _i64, _ptr],
+    ),
     "fi_selftest_mfma_f16": (ctypes.c_int, [_ptr, _ptr, _ptr, _ptr]),
 }
+
+# status words of the device block manager (state[2])
+FI_KV_OK = 0
+FI_KV_OUT_OF_BLOCKS = 1
+FI_KV_TABLE_FULL = 2
+FI_KV_NEGATIVE_COUNT = 3
 
 _lib = None
 _lock = threading.Lock()

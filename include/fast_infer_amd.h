@@ -193,6 +193,63 @@ FI_API int fi_rope_store_kv(const void* q, int64_t q_sb, int64_t q_st, int64_t q
                      void* stream);
 
 /*
+ * Device-resident block manager for the paged pool: per-sequence lengths and a FIFO
+ * queue of free blocks, served on the stream (no host round trip).  Replaces the host
+ * allocator kv_cache.py:50-63 as driven by model.py:172-174 (prefill) and :196-198
+ * (decode), and the single shared token count of model.py:169-170 / :193-194.
+ *
+ * State (int32 device arrays the caller allocates; fi_kv_reset initialises them):
+ *   block_table [rows, bt_stride]  logical -> physical block, -1 = unallocated; a row's
+ *                                  entries 0 .. num_alloc[b]-1 are valid
+ *   num_alloc   [rows]             blocks allocated to each row
+ *   seq_lens    [rows]             tokens stored in each row
+ *   free_queue  [num_blocks]       ring buffer of free block ids
+ *   state       [4]                {head, free count, status, row of the status}
+ * status is FI_KV_OK or the first error since the last reset (sticky):
+ */
+#define FI_KV_OK 0
+#define FI_KV_OUT_OF_BLOCKS 1  /* the queue ran out ("KV cache out of memory", :52-53) */
+#define FI_KV_TABLE_FULL 2     /* a row needs more than max_blocks_per_seq blocks (:58-59) */
+#define FI_KV_NEGATIVE_COUNT 3 /* a negative per-row token count */
+
+/*
+ * Add num_new[b] tokens (num_new_all for every row if num_new is NULL) to rows
+ * 0..batch-1: each row gets blocks until ceil(seq_lens[b] / block_size) are allocated,
+ * rows in order, each row's new blocks taken from the front of the free queue in logical
+ * order (the reference's free_blocks.pop(0) order).  The first row that cannot be served
+ * and every later row are left unchanged and the status records it.
+ *   start_pos_out[b] (optional): the row's length before the call = the position of its
+ *   first new token (fi_rope_store_kv's start_pos_per_seq);
+ *   context_lens_out[b] (optional): its length after the call (fi_paged_attention_fwd's
+ *   context_lens).
+ * One workgroup; a call is ordered after earlier work on the stream.
+ */
+FI_API int fi_kv_append(int32_t* block_table, int64_t bt_stride, int64_t max_blocks_per_seq,
+                 int32_t* num_alloc, int32_t* seq_lens, const int32_t* free_queue,
+                 int32_t* state, int64_t num_blocks, int64_t block_size,
+                 int64_t batch, const int32_t* num_new, int64_t num_new_all,
+                 int32_t* start_pos_out, int32_t* context_lens_out, void* stream);
+
+/*
+ * Release every row b < batch with release_rows[b] != 0: its blocks go to the back of
+ * the free queue in (row, logical block) order, its table entries become -1 and its
+ * length 0.  No counterpart in the reference, which only frees everything at once
+ * (kv_cache.py:108-113); needed to retire one sequence of a running batch.
+ */
+FI_API int fi_kv_release(int32_t* block_table, int64_t bt_stride, int64_t max_blocks_per_seq,
+                  int32_t* num_alloc, int32_t* seq_lens, int32_t* free_queue,
+                  int32_t* state, int64_t num_blocks, int64_t batch,
+                  const int32_t* release_rows, void* stream);
+
+/*
+ * kv_cache.py:108-113 (reset) for the device state: all max_batch rows' entries -1,
+ * lengths 0, free queue 0..num_blocks-1 in order, status FI_KV_OK.
+ */
+FI_API int fi_kv_reset(int32_t* block_table, int64_t bt_stride, int64_t max_blocks_per_seq,
+                int64_t max_batch, int32_t* num_alloc, int32_t* seq_lens,
+                int32_t* free_queue, int32_t* state, int64_t num_blocks, void* stream);
+
+/*
  * Self-test of the gfx950 MFMA fragment layout the attention kernels assume
  * (no counterpart in the reference; used by the test suite).  One wave computes
  * C[16x16] = A[16x32] * B[32x16] with v_mfma_f32_16x16x32_f16, where lane l holds

@@ -33,7 +33,7 @@ def lib():
 def test_header_declares_entry_points():
     names = _declared()
     for n in ("fi_flash_attention_fwd", "fi_paged_attention_fwd", "fi_kv_store",
-              "fi_rope_store_kv",
+              "fi_rope_store_kv", "fi_kv_append", "fi_kv_release", "fi_kv_reset",
               "fi_paged_attention_workspace_size", "fi_last_error", "fi_version"):
         assert n in names
 
@@ -131,6 +131,26 @@ def test_rope_store_kv_validation(lib):
     # empty calls return before touching any pointer
     assert lib.fi_rope_store_kv(*_rope_args(batch=0, q=None, k=None)) == _lib.FI_OK
     assert lib.fi_rope_store_kv(*_rope_args(tokens=0)) == _lib.FI_OK
+
+
+def test_block_manager_validation(lib):
+    from fast_infer_amd import _lib
+
+    st = (16, 16, 4, 16, 16, 16, 16)   # table, stride, max blocks, num_alloc, lens, queue, state
+    assert lib.fi_kv_append(None, *st[1:], 8, 16, 1, None, 1, None, None, None) == \
+        _lib.FI_ERR_INVALID
+    assert b"null" in lib.fi_last_error()
+    assert lib.fi_kv_append(*st, 0, 16, 1, None, 1, None, None, None) == _lib.FI_ERR_INVALID
+    assert lib.fi_kv_append(*st, 8, 0, 1, None, 1, None, None, None) == _lib.FI_ERR_INVALID
+    assert lib.fi_kv_append(*st, 8, 16, 1, None, -1, None, None, None) == _lib.FI_ERR_INVALID
+    # max_blocks_per_seq larger than the table stride
+    assert lib.fi_kv_append(16, 2, 4, 16, 16, 16, 16, 8, 16, 1, None, 1, None, None, None) == \
+        _lib.FI_ERR_INVALID
+    assert lib.fi_kv_release(*st, 8, 1, None, None) == _lib.FI_ERR_INVALID
+    assert lib.fi_kv_reset(16, 16, 4, 2, 16, 16, 16, None, 8, None) == _lib.FI_ERR_INVALID
+    # empty batches return before any launch
+    assert lib.fi_kv_append(*st, 8, 16, 0, None, 1, None, None, None) == _lib.FI_OK
+    assert lib.fi_kv_release(*st, 8, 0, None, None) == _lib.FI_OK
 
 
 def test_workspace_size(lib):
