@@ -13,6 +13,8 @@ serve them.  The same line carries:
 * ``decode_b1_ctx256`` / ``prefill_b1_s512`` — the small configurations (latency);
 * ``decode_step_28layer_b64_paged`` — the same step with the device block manager (one
   append per step) and the fused RoPE + pool write per layer before attention;
+* ``int4_linear`` — the INT4 QKV / O projections around attention (decode batch 64 and 1
+  over 28 layers of weights, GB/s; prefill QKV at 16384 tokens, TFLOP/s);
 * ``rope_store_kv`` — the fused RoPE + K/V pool write (batch 4 x 4096 prefill, batch 64
   decode), GB/s of algorithmic traffic;
 * ``decode_28layer_b64`` — a 28-layer decode step over per-layer pools, batch 64,
@@ -50,7 +52,8 @@ def _args():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", default="", help="comma list: decode,prefill,small,e2e,rope")
+    ap.add_argument("--only", default="",
+                    help="comma list: decode,prefill,small,e2e,rope,int4")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device copy (reference for PMC byte counters)")
     return ap.parse_args()
@@ -278,6 +281,43 @@ def bench_decode_step_paged(torch, fi, timer, steps, warmup, dev):
     return dict(t=t, bytes=nbytes, gbs=nbytes / t / 1e9, tok_s=B / t, tokens=sum(mid))
 
 
+def bench_int4(torch, fi, timer, steps, warmup, dev):
+    """INT4 QKV (N 5120) and O (N 3072) projections, K 3072, over 28 layers' weights (364
+    MB packed, past the 256 MB last-level cache): decode at batch 64 and batch 1, and
+    prefill at 4 x 4096 tokens."""
+    from fast_infer_amd import roofline as R
+
+    L, K, NQKV, NO = 28, 3072, (HQ + 2 * HKV) * D, HQ * D
+    g = torch.Generator(device=dev).manual_seed(5)
+    layers = []
+    for _ in range(L):
+        wq = (torch.randn(NQKV, K, device=dev, generator=g) * 0.02).half()
+        wo = (torch.randn(NO, K, device=dev, generator=g) * 0.02).half()
+        layers.append((fi.quantize_int4_groupwise(wq), fi.quantize_int4_groupwise(wo)))
+        del wq, wo
+    res = {}
+    for M in (64, 1):
+        x = torch.randn(M, K, device=dev, generator=g).half()
+        ws = torch.empty(max(fi._lib.load().fi_int4_matmul_workspace_size(M, n, K)
+                             for n in (NQKV, NO)) or 1, dtype=torch.uint8, device=dev)
+
+        def step():
+            for wqkv, wo in layers:
+                fi.int4_matmul(x, wqkv, workspace=ws)
+                fi.int4_matmul(x, wo, workspace=ws)
+
+        t = timer.run(step, max(1, steps // 10), max(1, warmup // 5))
+        nbytes = L * (R.int4_matmul_bytes(M, NQKV, K) + R.int4_matmul_bytes(M, NO, K))
+        res[f"decode_b{M}"] = dict(t=t, bytes=nbytes, gbs=nbytes / t / 1e9)
+    M = 4 * 4096
+    x = torch.randn(M, K, device=dev, generator=g).half()
+    wqkv = layers[0][0]
+    t = timer.run(lambda: fi.int4_matmul(x, wqkv), max(1, steps // 10), max(1, warmup // 5))
+    fl = R.matmul_flops(M, NQKV, K)
+    res["prefill_qkv"] = dict(t=t, flops=fl, tflops=fl / t / 1e12)
+    return res
+
+
 # ----------------------------------------------------------------------------- CPU
 
 
@@ -353,7 +393,8 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     timer = Timer(torch)
-    only = set(filter(None, a.only.split(","))) or {"decode", "prefill", "small", "e2e", "rope"}
+    only = set(filter(None, a.only.split(","))) or {"decode", "prefill", "small", "e2e", "rope",
+                                                    "int4"}
     cores = _cores()
     steps, warm = a.steps, a.warmup
     out = {"metric": METRIC}
@@ -453,6 +494,26 @@ def main():
                            "algorithmic_bytes": rd["bytes"]}}
         print(f"[bench] rope+store b4 s4096: {rp['t'] * 1e6:.1f} us, {rp['gbs']:.0f} GB/s; "
               f"decode b64 {rd['t'] * 1e6:.2f} us", file=sys.stderr, flush=True)
+
+    if "int4" in only:
+        q = bench_int4(torch, fi, timer, steps, warm, dev)
+        d64, d1, pq = q["decode_b64"], q["decode_b1"], q["prefill_qkv"]
+        out["int4_linear"] = {
+            "workload": "INT4 QKV (N 5120) + O (N 3072) projections, K 3072, groupsize 128, "
+                        "over 28 layers of weights (364 MB packed); prefill: QKV at 4 x 4096 "
+                        "tokens",
+            "decode_b64": {"us_per_layer": round(d64["t"] / 28 * 1e6, 2),
+                           "GB/s": round(d64["gbs"], 1),
+                           "frac_hbm": round(d64["gbs"] / R.HBM_PEAK_GBS, 4)},
+            "decode_b1": {"us_per_layer": round(d1["t"] / 28 * 1e6, 2),
+                          "GB/s": round(d1["gbs"], 1),
+                          "frac_hbm": round(d1["gbs"] / R.HBM_PEAK_GBS, 4)},
+            "prefill_qkv_m16384": {"us_per_call": round(pq["t"] * 1e6, 1),
+                                   "TFLOP/s": round(pq["tflops"], 1),
+                                   "frac_mfma": round(pq["tflops"] / R.FP16_MFMA_PEAK_TFLOPS, 4)}}
+        print(f"[bench] int4 decode b64 {d64['t'] / 28 * 1e6:.2f} us/layer {d64['gbs']:.0f} GB/s; "
+              f"b1 {d1['t'] / 28 * 1e6:.2f} us/layer {d1['gbs']:.0f} GB/s; prefill qkv "
+              f"{pq['t'] * 1e6:.0f} us {pq['tflops']:.0f} TFLOP/s", file=sys.stderr, flush=True)
 
     if not a.no_cpu_baseline:
         if dec is not None:

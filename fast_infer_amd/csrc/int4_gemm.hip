@@ -1,0 +1,591 @@
+// INT4 group-quantized linear layers for gfx950: quantize, dequantize, and C = X * W^T
+// with the dequantization fused into the MFMA loop.
+//
+// Wire format (loader.py:9-41): W [N, K] is stored as int8 bytes [N, K/2]; byte j of a
+// row holds k = 2j in its low nibble and k = 2j+1 in its high nibble, each a 4-bit two's
+// complement value in [-8, 7]; scales are fp16 [N, K/128], one per 128-wide group.
+// The weight the reference multiplies with is fp16(q * scale) (matmul.py:83-84 and
+// :197-214): one rounding of an exact product, which is what v_pk_mul_f16 computes.
+//
+// GEMM: C[m, n] = fp16( sum_k X[m, k] * W[n, k] ), fp32 accumulation (matmul.py:14-132,
+// :135-186).  One workgroup = 4 waves = 64 output columns (16 per wave) x MT rows, over a
+// slice of the K groups.  Per 128-wide group, X[MT, 128] is staged in LDS (double
+// buffered, rows padded to 272 bytes so the 16 rows a wave reads are on distinct banks);
+// each lane loads 16 bytes of its weight row (32 int4 values), dequantizes them in
+// registers and feeds v_mfma_f32_16x16x32_f16 with W as the A operand and X^T as the B
+// operand.  In k-step s (0..3) of a group, lane group g = lane/16 supplies k = 32g + 8s
+// .. +7: the 16 bytes one lane loads are exactly its four k-steps.  Small grids split the
+// K groups over blockIdx.z; a second kernel adds the fp32 partials in a fixed order.
+#include <stdlib.h>
+
+#include <algorithm>
+
+#include "common.h"
+
+namespace fi {
+namespace gemm {
+
+constexpr int kThreads = 256;
+constexpr int kNTile = 64;
+constexpr int kGroup = 128;     // K per scale group and per pipeline step
+constexpr int kLdsRow = 136;    // halves per staged X row (128 + 8 pad)
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+struct Params {
+  const half_t* x;
+  int64_t x_stride;  // elements between rows of X
+  int M, K, N;
+  const uint8_t* w;  // int4 bytes [N, K/2] or fp16 [N, K]
+  int64_t w_stride;  // bytes (int4) or elements (fp16) between rows of W
+  const half_t* scales;
+  int64_t s_stride;  // elements between rows of scales
+  half_t* out;
+  int64_t out_stride;
+  float* partial;    // [splits, M, N] fp32 when splits > 1
+  int groups_per_split;
+};
+
+__device__ __forceinline__ uint32_t as_u32(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
+__device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
+
+// Eight int4 values (natural k order, nibble i = k0 + i) -> fp16(q * s).
+__device__ __forceinline__ half8 dequant8(uint32_t d, half2_t s2) {
+#pragma clang fp contract(off)
+  d ^= 0x88888888u;  // two's complement nibble n -> n + 8 in [0, 15]
+  // 0x6400 | v is the fp16 value 1024 + v; minus 1032 gives the signed nibble exactly
+  const half2_t bias = {(half_t)1032.0f, (half_t)1032.0f};
+  const half2_t p0 = (as_h2((d & 0x000F000Fu) | 0x64006400u) - bias) * s2;          // k0, k4
+  const half2_t p1 = (as_h2(((d >> 4) & 0x000F000Fu) | 0x64006400u) - bias) * s2;   // k1, k5
+  const half2_t p2 = (as_h2(((d >> 8) & 0x000F000Fu) | 0x64006400u) - bias) * s2;   // k2, k6
+  const half2_t p3 = (as_h2(((d >> 12) & 0x000F000Fu) | 0x64006400u) - bias) * s2;  // k3, k7
+  u32x4 r;
+  r[0] = __builtin_amdgcn_perm(as_u32(p1), as_u32(p0), 0x05040100u);  // k0, k1
+  r[1] = __builtin_amdgcn_perm(as_u32(p3), as_u32(p2), 0x05040100u);  // k2, k3
+  r[2] = __builtin_amdgcn_perm(as_u32(p1), as_u32(p0), 0x07060302u);  // k4, k5
+  r[3] = __builtin_amdgcn_perm(as_u32(p3), as_u32(p2), 0x07060302u);  // k6, k7
+  return as_half8(r);
+}
+
+// Store a workgroup's 64-column x (16 * kMSub)-row tile.  Lane (row, grp) of wave w holds
+// C[m0 + 16j + row][n0 + 16w + 4grp + i] in acc[j][i].  With K split over blockIdx.z the
+// tile goes to the fp32 partials (reduce_kernel adds them), otherwise to the fp16 output.
+template <int kMSub>
+__device__ __forceinline__ void store_tile(const Params& p, const floatx4 (&acc)[kMSub], int m0,
+                                           int n0) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int row = lane & 15;
+  const int nb = n0 + wave * 16 + 4 * (lane >> 4);
+#pragma unroll
+  for (int j = 0; j < kMSub; ++j) {
+    const int m = m0 + 16 * j + row;
+    if (m >= p.M) continue;
+    if (p.partial) {
+      float* dst = p.partial + ((int64_t)blockIdx.z * p.M + m) * p.N + nb;
+      if (nb + 3 < p.N && (p.N & 3) == 0) {
+        *(floatx4*)dst = acc[j];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (nb + i < p.N) dst[i] = acc[j][i];
+      }
+    } else {
+      half_t* dst = p.out + (int64_t)m * p.out_stride + nb;
+      const half4 h = to_half4(acc[j]);
+      if (nb + 3 < p.N && ((uintptr_t)dst & 7) == 0) {
+        *(half4*)dst = h;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (nb + i < p.N) dst[i] = h[i];
+      }
+    }
+  }
+}
+
+template <int MT, bool kInt4>
+__global__ __launch_bounds__(kThreads, 2) void gemm_kernel(Params p) {
+  constexpr int kMSub = MT / 16;          // 16-row MFMA tiles per wave
+  constexpr int kXLoads = MT / 16;        // 16-byte X loads per thread per group
+  __shared__ __attribute__((aligned(16))) half_t xs[2][MT * kLdsRow];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int row = lane & 15;
+  const int grp = lane >> 4;
+  const int n = blockIdx.x * kNTile + wave * 16 + row;  // this lane's weight row
+  const int nc = n < p.N ? n : p.N - 1;                 // rows past N compute, never store
+  const int m0 = blockIdx.y * MT;
+  const int groups = p.K / kGroup;
+  const int g_begin = blockIdx.z * p.groups_per_split;
+  const int g_end = min(g_begin + p.groups_per_split, groups);
+
+  // X staging: thread t moves 16 bytes of rows t/16 + 16i, chunk t%16
+  const int xr = threadIdx.x >> 4;
+  const int xc = threadIdx.x & 15;
+  u32x4 xreg[kXLoads];
+  auto load_x = [&](int g) {
+#pragma unroll
+    for (int i = 0; i < kXLoads; ++i) {
+      const int m = m0 + xr + 16 * i;
+      if (m < p.M)
+        xreg[i] = *(const u32x4*)(p.x + (int64_t)m * p.x_stride + g * kGroup + xc * 8);
+      else
+        xreg[i] = u32x4{0, 0, 0, 0};
+    }
+  };
+  auto store_x = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < kXLoads; ++i)
+      *(u32x4*)(&xs[buf][(xr + 16 * i) * kLdsRow + xc * 8]) = xreg[i];
+  };
+
+  // weights of this lane for one group: 16 bytes (int4) or 4 x 16 bytes (fp16)
+  u32x4 wreg[kInt4 ? 1 : 4];
+  half_t sreg = (half_t)0.0f;
+  auto load_w = [&](int g) {
+    if constexpr (kInt4) {
+      wreg[0] = *(const u32x4*)(p.w + (int64_t)nc * p.w_stride + g * (kGroup / 2) + grp * 16);
+      sreg = p.scales[(int64_t)nc * p.s_stride + g];
+    } else {
+      const half_t* wr = (const half_t*)p.w + (int64_t)nc * p.w_stride + g * kGroup + grp * 32;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) wreg[s] = *(const u32x4*)(wr + 8 * s);
+    }
+  };
+
+  floatx4 acc[kMSub];
+#pragma unroll
+  for (int j = 0; j < kMSub; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  if (g_begin < g_end) {
+    load_x(g_begin);
+    load_w(g_begin);
+  }
+  int buf = 0;
+  for (int g = g_begin; g < g_end; ++g) {
+    store_x(buf);
+    __syncthreads();
+    half8 wf[4];
+    if constexpr (kInt4) {
+      const half2_t s2 = {sreg, sreg};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) wf[s] = dequant8(wreg[0][s], s2);
+    } else {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) wf[s] = as_half8(wreg[s]);
+    }
+    if (g + 1 < g_end) {  // next group's loads overlap this group's MFMAs
+      load_x(g + 1);
+      load_w(g + 1);
+    }
+    const half_t* xb = &xs[buf][row * kLdsRow + grp * 32];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+#pragma unroll
+      for (int j = 0; j < kMSub; ++j) {
+        const half8 xf = as_half8(*(const u32x4*)(xb + j * 16 * kLdsRow + 8 * s));
+        acc[j] = mfma16x16x32(wf[s], xf, acc[j]);
+      }
+    }
+    buf ^= 1;
+  }
+
+  store_tile<kMSub>(p, acc, m0, blockIdx.x * kNTile);
+}
+
+// Decode-sized calls (16 rows of X per blockIdx.y): one workgroup per 16 output columns.
+// The four waves take interleaved groups (g = wave, wave + 4, ...), so K is split inside
+// the workgroup and no partials leave it.  Each lane issues the loads of kChunk groups at
+// once (16 weight bytes, the scale, and 64 bytes of its X row per group) before any math,
+// so one memory latency covers the chunk; the four waves' sums are added through LDS in
+// a fixed order.
+template <bool kInt4, int kChunk>
+__global__ __launch_bounds__(kThreads) void gemv_kernel(Params p) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int row = lane & 15;
+  const int grp = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int n = n0 + row;
+  const int nc = n < p.N ? n : p.N - 1;
+  const int m = blockIdx.y * 16 + row;  // the X row this lane supplies
+  const bool m_ok = m < p.M;
+  // rows past M load a valid row: MFMA output column j depends on X row j only, and the
+  // columns of rows past M are never stored
+  const int mc = m_ok ? m : p.M - 1;
+  const int groups = p.K / kGroup;
+
+  floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int g0 = wave; g0 < groups; g0 += 4 * kChunk) {
+    // every load of the chunk is issued before any math and without branches (groups past
+    // the end reload the last group and are skipped below), so one latency covers them
+    u32x4 wv[kInt4 ? kChunk : 4 * kChunk];
+    half_t sv[kChunk];
+    u32x4 xv[4 * kChunk];
+#pragma unroll
+    for (int c = 0; c < kChunk; ++c) {
+      const int g = min(g0 + 4 * c, groups - 1);
+      if constexpr (kInt4) {
+        wv[c] = *(const u32x4*)(p.w + (int64_t)nc * p.w_stride + g * (kGroup / 2) + grp * 16);
+        sv[c] = p.scales[(int64_t)nc * p.s_stride + g];
+      } else {
+        const half_t* wr = (const half_t*)p.w + (int64_t)nc * p.w_stride + g * kGroup + grp * 32;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) wv[4 * c + s] = *(const u32x4*)(wr + 8 * s);
+      }
+      const half_t* xr = p.x + (int64_t)mc * p.x_stride + g * kGroup + grp * 32;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) xv[4 * c + s] = *(const u32x4*)(xr + 8 * s);
+    }
+#pragma unroll
+    for (int c = 0; c < kChunk; ++c) {
+      if (g0 + 4 * c < groups) {  // uniform across the wave
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          half8 wf;
+          if constexpr (kInt4)
+            wf = dequant8(wv[c][s], half2_t{sv[c], sv[c]});
+          else
+            wf = as_half8(wv[4 * c + s]);
+          acc = mfma16x16x32(wf, as_half8(xv[4 * c + s]), acc);
+        }
+      }
+    }
+  }
+
+  __shared__ floatx4 red[4][64];
+  red[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0) {
+    floatx4 t = red[0][lane];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) t += red[w][lane];
+    if (m_ok) {
+      const int nb = n0 + 4 * grp;
+      half_t* dst = p.out + (int64_t)m * p.out_stride + nb;
+      const half4 h = to_half4(t);
+      if (nb + 3 < p.N && ((uintptr_t)dst & 7) == 0) {
+        *(half4*)dst = h;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (nb + i < p.N) dst[i] = h[i];
+      }
+    }
+  }
+}
+
+// out[m, n] = fp16(sum over splits of partial[s, m, n]), splits added in order.
+__global__ __launch_bounds__(256) void reduce_kernel(const float* partial, int splits, int M,
+                                                     int N, half_t* out, int64_t out_stride) {
+  const int64_t total = (int64_t)M * N;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    float s = 0.f;
+    for (int k = 0; k < splits; ++k) s += __builtin_nontemporal_load(partial + k * total + i);
+    const int m = (int)(i / N);
+    const int nn = (int)(i - (int64_t)m * N);
+    out[(int64_t)m * out_stride + nn] = (half_t)s;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// loader.py:9-41: symmetric groupwise INT4 quantization, with the reference's fp16 tensor
+// arithmetic: amax = max|w| over the group (fp16), clamped below at fp16(1e-6); scale =
+// fp16(fp32(amax) * fp32(1/7)) (torch multiplies by the reciprocal when a CUDA tensor is
+// divided by a Python scalar); q = round_half_even(fp16(fp32(w) / fp32(scale))), clamped to
+// [-8, 7].  16 lanes per group, 8 values per lane.
+__global__ __launch_bounds__(256) void quantize_kernel(const half_t* w, int64_t w_stride, int N,
+                                                       int K, uint8_t* packed,
+                                                       int64_t p_stride, half_t* scales,
+                                                       int64_t s_stride) {
+  const int groups = K / kGroup;
+  const int64_t total = (int64_t)N * groups;
+  const int lane16 = threadIdx.x & 15;
+  for (int64_t gi = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4; gi < total;
+       gi += ((int64_t)gridDim.x * blockDim.x) >> 4) {
+    const int nrow = (int)(gi / groups);
+    const int g = (int)(gi - (int64_t)nrow * groups);
+    const half8 v = as_half8(
+        *(const u32x4*)(w + (int64_t)nrow * w_stride + g * kGroup + lane16 * 8));
+    float amax = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf((float)v[e]));
+#pragma unroll
+    for (int d = 1; d < 16; d <<= 1) amax = fmaxf(amax, __shfl_xor(amax, d, 16));
+    const float lo = (float)(half_t)1e-6f;
+    amax = fmaxf(amax, lo);
+    const half_t scale = (half_t)(amax * (1.0f / 7.0f));
+    const float sf = (float)scale;
+    uint32_t word = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float qf = (float)(half_t)((float)v[e] / sf);
+      const float qr = fminf(fmaxf(__builtin_rintf(qf), -8.f), 7.f);
+      word |= ((uint32_t)(int)qr & 0xFu) << (4 * e);
+    }
+    *(uint32_t*)(packed + (int64_t)nrow * p_stride + g * (kGroup / 2) + lane16 * 4) = word;
+    if (lane16 == 0) scales[(int64_t)nrow * s_stride + g] = scale;
+  }
+}
+
+// matmul.py:197-214 (_dequant_storage): W = fp16(q * scale), 8 values per thread.
+__global__ __launch_bounds__(256) void dequantize_kernel(const uint8_t* packed, int64_t p_stride,
+                                                         const half_t* scales, int64_t s_stride,
+                                                         int N, int K, half_t* w,
+                                                         int64_t w_stride) {
+  const int per_row = K / 8;
+  const int64_t total = (int64_t)N * per_row;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int nrow = (int)(i / per_row);
+    const int c = (int)(i - (int64_t)nrow * per_row);
+    const uint32_t d = *(const uint32_t*)(packed + (int64_t)nrow * p_stride + c * 4);
+    const half_t s = scales[(int64_t)nrow * s_stride + (c * 8) / kGroup];
+    *(u32x4*)(w + (int64_t)nrow * w_stride + c * 8) = as_u32x4(dequant8(d, half2_t{s, s}));
+  }
+}
+
+// Kernel, tile rows and split count for an (M, N, K) call; shared by the size query and
+// the launch.  gemv_rows: X rows per gemv launch row (0 = use the tiled kernel).
+struct Plan {
+  int mt;
+  int splits;
+  int gemv_rows;
+};
+
+inline int gemv_limit() {
+  static int v = [] {
+    const char* e = getenv("FI_INT4_GEMV_MAX_M");
+    return e ? atoi(e) : 16;
+  }();
+  return v;
+}
+
+inline int env_int(const char* name, int dflt) {
+  const char* e = getenv(name);
+  return e ? atoi(e) : dflt;
+}
+
+inline Plan plan(int64_t M, int64_t N, int64_t K) {
+  Plan pl;
+  pl.gemv_rows = 0;
+  if (M <= gemv_limit() && (M + 15) / 16 <= 65535) {
+    pl.gemv_rows = 16;
+    pl.mt = 16;
+    pl.splits = 1;
+    return pl;
+  }
+  const int64_t groups = K / kGroup;
+  pl.mt = M <= 16 ? 16 : M <= 32 ? 32 : M <= 64 ? 64 : 128;
+  const int64_t wgs = ((N + kNTile - 1) / kNTile) * ((M + pl.mt - 1) / pl.mt);
+  int64_t s = 1;
+  if (wgs < 256) {
+    s = (512 + wgs - 1) / wgs;
+    // keep the fp32 partials (written and read once) below the weight bytes
+    const int64_t cap = std::max<int64_t>(1, K / (16 * std::max<int64_t>(M, 1)));
+    s = std::min<int64_t>(std::min<int64_t>(s, cap), groups);
+  }
+  static const int forced = env_int("FI_INT4_SPLITS", 0);
+  if (forced > 0) s = std::min<int64_t>(forced, groups);
+  // every split gets the same whole number of groups
+  const int64_t per = (groups + s - 1) / std::max<int64_t>(s, 1);
+  pl.splits = (int)((groups + per - 1) / std::max<int64_t>(per, 1));
+  if (pl.splits < 1) pl.splits = 1;
+  return pl;
+}
+
+}  // namespace gemm
+}  // namespace fi
+
+extern "C" size_t fi_int4_matmul_workspace_size(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % fi::gemm::kGroup) return 0;
+  const fi::gemm::Plan pl = fi::gemm::plan(M, N, K);
+  return pl.splits > 1 ? (size_t)pl.splits * M * N * sizeof(float) : 0;
+}
+
+extern "C" int fi_int4_matmul(const void* x, int64_t x_stride, int64_t M, int64_t K,
+                              const void* w, int64_t w_stride, const void* scales,
+                              int64_t s_stride, int64_t N, int64_t groupsize, void* out,
+                              int64_t out_stride, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+  using namespace fi;
+  using namespace fi::gemm;
+  clear_error();
+  if (M < 0 || N < 0 || K < 0) {
+    set_error("fi_int4_matmul: negative size");
+    return FI_ERR_INVALID;
+  }
+  if (M == 0 || N == 0) return FI_OK;
+  const bool int4 = scales != nullptr;
+  if (int4 && groupsize != kGroup) {
+    set_error("fi_int4_matmul: groupsize %lld not supported (only %d)", (long long)groupsize,
+              kGroup);
+    return FI_ERR_UNSUPPORTED;
+  }
+  if (K == 0 || K % kGroup) {
+    set_error("fi_int4_matmul: K %lld must be a positive multiple of %d", (long long)K, kGroup);
+    return FI_ERR_UNSUPPORTED;
+  }
+  if (M >= (1ll << 30) || N >= (1ll << 30) || K >= (1ll << 30)) {
+    set_error("fi_int4_matmul: sizes too large");
+    return FI_ERR_UNSUPPORTED;
+  }
+  if (!x || !w || !out) {
+    set_error("fi_int4_matmul: null pointer");
+    return FI_ERR_INVALID;
+  }
+  const bool x_ok = ((uintptr_t)x & 15) == 0 && x_stride % 8 == 0 && x_stride >= K;
+  const bool w_ok = int4 ? (((uintptr_t)w & 15) == 0 && w_stride % 16 == 0 && w_stride >= K / 2 &&
+                            ((uintptr_t)scales & 1) == 0 && s_stride >= K / kGroup)
+                         : (((uintptr_t)w & 15) == 0 && w_stride % 8 == 0 && w_stride >= K);
+  if (!x_ok || !w_ok || ((uintptr_t)out & 1) || out_stride < N) {
+    set_error("fi_int4_matmul: rows must be 16-byte aligned and strides cover the rows "
+              "(x_stride %lld, w_stride %lld, out_stride %lld)", (long long)x_stride,
+              (long long)w_stride, (long long)out_stride);
+    return FI_ERR_INVALID;
+  }
+  const Plan pl = plan(M, N, K);
+  hipStream_t st = (hipStream_t)stream;
+  if (pl.gemv_rows) {
+    Params p;
+    p.x = (const half_t*)x;
+    p.x_stride = x_stride;
+    p.M = (int)M;
+    p.K = (int)K;
+    p.N = (int)N;
+    p.w = (const uint8_t*)w;
+    p.w_stride = w_stride;
+    p.scales = (const half_t*)scales;
+    p.s_stride = s_stride;
+    p.out = (half_t*)out;
+    p.out_stride = out_stride;
+    p.partial = nullptr;
+    p.groups_per_split = (int)(K / kGroup);
+    const dim3 grid((unsigned)((N + 15) / 16), (unsigned)((M + 15) / 16), 1);
+    if (int4)
+      hipLaunchKernelGGL((gemv_kernel<true, 6>), grid, dim3(kThreads), 0, st, p);
+    else
+      hipLaunchKernelGGL((gemv_kernel<false, 3>), grid, dim3(kThreads), 0, st, p);
+    return check_launch("fi_int4_matmul");
+  }
+  const size_t need = pl.splits > 1 ? (size_t)pl.splits * M * N * sizeof(float) : 0;
+  if (need && (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 15))) {
+    set_error("fi_int4_matmul: workspace of %zu bytes needed (have %zu)", need,
+              workspace ? workspace_bytes : (size_t)0);
+    return FI_ERR_WORKSPACE;
+  }
+  Params p;
+  p.x = (const half_t*)x;
+  p.x_stride = x_stride;
+  p.M = (int)M;
+  p.K = (int)K;
+  p.N = (int)N;
+  p.w = (const uint8_t*)w;
+  p.w_stride = w_stride;
+  p.scales = (const half_t*)scales;
+  p.s_stride = s_stride;
+  p.out = (half_t*)out;
+  p.out_stride = out_stride;
+  p.partial = pl.splits > 1 ? (float*)workspace : nullptr;
+  const int groups = (int)(K / kGroup);
+  p.groups_per_split = (groups + pl.splits - 1) / pl.splits;
+  const dim3 grid((unsigned)((N + kNTile - 1) / kNTile), (unsigned)((M + pl.mt - 1) / pl.mt),
+                  (unsigned)pl.splits);
+  if (grid.y > 65535) {
+    set_error("fi_int4_matmul: M %lld too large", (long long)M);
+    return FI_ERR_UNSUPPORTED;
+  }
+#define FI_GEMM_LAUNCH(MT)                                                                \
+  do {                                                                                  \
+    if (int4)                                                                           \
+      hipLaunchKernelGGL((gemm_kernel<MT, true>), grid, dim3(kThreads), 0, st, p);       \
+    else                                                                                \
+      hipLaunchKernelGGL((gemm_kernel<MT, false>), grid, dim3(kThreads), 0, st, p);      \
+  } while (0)
+  {
+    switch (pl.mt) {
+      case 16: FI_GEMM_LAUNCH(16); break;
+      case 32: FI_GEMM_LAUNCH(32); break;
+      case 64: FI_GEMM_LAUNCH(64); break;
+      default: FI_GEMM_LAUNCH(128); break;
+    }
+  }
+#undef FI_GEMM_LAUNCH
+  if (pl.splits > 1) {
+    const int64_t total = M * N;
+    const int64_t blocks = std::min<int64_t>((total + 255) / 256, 4096);
+    hipLaunchKernelGGL(reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
+                       (const float*)workspace, pl.splits, (int)M, (int)N, (half_t*)out,
+                       out_stride);
+  }
+  return check_launch("fi_int4_matmul");
+}
+
+extern "C" int fi_int4_quantize(const void* w, int64_t w_stride, int64_t N, int64_t K,
+                                int64_t groupsize, void* packed, int64_t p_stride,
+                                void* scales, int64_t s_stride, void* stream) {
+  using namespace fi;
+  using namespace fi::gemm;
+  clear_error();
+  if (groupsize != kGroup) {
+    set_error("fi_int4_quantize: groupsize %lld not supported (only %d)", (long long)groupsize,
+              kGroup);
+    return FI_ERR_UNSUPPORTED;
+  }
+  if (N < 0 || K < 0 || K % kGroup || N >= (1ll << 30) || K >= (1ll << 30)) {
+    set_error("fi_int4_quantize: invalid sizes N %lld K %lld", (long long)N, (long long)K);
+    return FI_ERR_INVALID;
+  }
+  if (N == 0 || K == 0) return FI_OK;
+  if (!w || !packed || !scales) {
+    set_error("fi_int4_quantize: null pointer");
+    return FI_ERR_INVALID;
+  }
+  if (((uintptr_t)w & 15) || w_stride % 8 || w_stride < K || ((uintptr_t)packed & 3) ||
+      p_stride % 4 || p_stride < K / 2 || ((uintptr_t)scales & 1) || s_stride < K / kGroup) {
+    set_error("fi_int4_quantize: misaligned rows or short strides");
+    return FI_ERR_INVALID;
+  }
+  const int64_t lanes = N * (K / kGroup) * 16;
+  const int64_t blocks = std::min<int64_t>((lanes + 255) / 256, 65536);
+  hipLaunchKernelGGL(quantize_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                     (const half_t*)w, w_stride, (int)N, (int)K, (uint8_t*)packed, p_stride,
+                     (half_t*)scales, s_stride);
+  return check_launch("fi_int4_quantize");
+}
+
+extern "C" int fi_int4_dequantize(const void* packed, int64_t p_stride, const void* scales,
+                                  int64_t s_stride, int64_t N, int64_t K, int64_t groupsize,
+                                  void* w, int64_t w_stride, void* stream) {
+  using namespace fi;
+  using namespace fi::gemm;
+  clear_error();
+  if (groupsize != kGroup) {
+    set_error("fi_int4_dequantize: groupsize %lld not supported (only %d)",
+              (long long)groupsize, kGroup);
+    return FI_ERR_UNSUPPORTED;
+  }
+  if (N < 0 || K < 0 || K % kGroup || N >= (1ll << 30) || K >= (1ll << 30)) {
+    set_error("fi_int4_dequantize: invalid sizes N %lld K %lld", (long long)N, (long long)K);
+    return FI_ERR_INVALID;
+  }
+  if (N == 0 || K == 0) return FI_OK;
+  if (!w || !packed || !scales) {
+    set_error("fi_int4_dequantize: null pointer");
+    return FI_ERR_INVALID;
+  }
+  if (((uintptr_t)w & 15) || w_stride % 8 || w_stride < K || ((uintptr_t)packed & 3) ||
+      p_stride % 4 || p_stride < K / 2 || ((uintptr_t)scales & 1) || s_stride < K / kGroup) {
+    set_error("fi_int4_dequantize: misaligned rows or short strides");
+    return FI_ERR_INVALID;
+  }
+  const int64_t items = N * (K / 8);
+  const int64_t blocks = std::min<int64_t>((items + 255) / 256, 65536);
+  hipLaunchKernelGGL(dequantize_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                     (hipStream_t)stream, (const uint8_t*)packed, p_stride,
+                     (const half_t*)scales, s_stride, (int)N, (int)K, (half_t*)w, w_stride);
+  return check_launch("fi_int4_dequantize");
+}

@@ -1,0 +1,140 @@
+"""INT4 group-quantized linear layers (kernels/matmul.py, loader.py:9-41) on gfx950.
+
+``int4_matmul(x, w, scales=None, groupsize=128)`` keeps the reference's signature
+(kernels/matmul.py:217-231): ``w`` is either a ``(packed_int8, scales)`` tuple — the
+dequantization then runs inside the MFMA loop — or an fp16 ``[N, K]`` weight.
+``quantize_int4_groupwise`` (loader.py:9-41) and ``dequantize_int4`` (the reference's
+``_dequant_storage``, matmul.py:197-214) produce and expand the same wire format, bit for
+bit.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+
+def _need_cuda(name: str, t: torch.Tensor) -> None:
+    if t.device.type != "cuda":
+        raise RuntimeError(f"{name} must be on a HIP device; fast_infer_amd has no CPU path")
+
+
+def _rows16(t: torch.Tensor, elem: int) -> torch.Tensor:
+    """t with unit inner stride, 16-byte aligned rows and row stride a multiple of 16 B."""
+    if (t.stride(-1) != 1 or t.data_ptr() % 16 or (t.stride(0) * elem) % 16
+            or t.stride(0) < t.shape[1]):
+        t = t.contiguous()
+        if t.data_ptr() % 16 or (t.stride(0) * elem) % 16:
+            raise ValueError("rows must be 16-byte aligned (K a multiple of 8 elements)")
+    return t
+
+
+# Split-K calls need a workspace for their fp32 partials; one per (device, stream), grown
+# on demand, so back-to-back calls on a stream reuse it.
+_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
+
+
+def int4_matmul(x: torch.Tensor, w, scales=None, groupsize: int = 128, *,
+                workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """fp16 ``x [..., K]`` times a weight ``[N, K]`` -> fp16 ``[..., N]``
+    (kernels/matmul.py:217-231).  ``w`` is ``(packed int8 [N, K/2], scales fp16 [N,
+    K/groupsize])`` or an fp16 ``[N, K]`` tensor; ``scales`` is ignored as in the
+    reference.  Accumulation is fp32, the output rounded to fp16 once.  ``workspace``
+    (optional) must not be shared by calls that overlap in time; by default one cached
+    workspace per device and stream is used."""
+    _need_cuda("x", x)
+    if isinstance(w, tuple):
+        packed, sc = w
+        _need_cuda("packed", packed)
+        if packed.dtype not in (torch.int8, torch.uint8) or packed.dim() != 2:
+            raise TypeError("packed weights must be a 2-D int8 tensor")
+        if sc.dtype != torch.float16 or sc.dim() != 2:
+            raise TypeError("scales must be a 2-D float16 tensor")
+        N, K = packed.shape[0], packed.shape[1] * 2
+        if sc.shape[0] != N or sc.shape[1] * groupsize != K:
+            raise ValueError(f"scales {tuple(sc.shape)} do not match packed {tuple(packed.shape)}")
+        wt = _rows16(packed, 1)
+        if sc.stride(-1) != 1:
+            sc = sc.contiguous()
+        w_stride, s_ptr, s_stride = wt.stride(0), sc.data_ptr(), sc.stride(0)
+    else:
+        _need_cuda("w", w)
+        if w.dtype != torch.float16 or w.dim() != 2:
+            raise TypeError("w must be a 2-D float16 tensor or a (packed, scales) tuple")
+        N, K = w.shape
+        wt = _rows16(w, 2)
+        w_stride, s_ptr, s_stride = wt.stride(0), None, 0
+    if x.shape[-1] != K:
+        raise ValueError(f"x has K = {x.shape[-1]}, the weight K = {K}")
+    if K % groupsize:
+        raise ValueError(f"K ({K}) must be multiple of groupsize ({groupsize})")
+    if x.dtype != torch.float16:
+        x = x.to(torch.float16)
+    lead = x.shape[:-1]
+    x2 = _rows16(x.reshape(-1, K), 2)
+    M = x2.shape[0]
+    out = torch.empty(M, N, dtype=torch.float16, device=x.device)
+    if M == 0 or N == 0:
+        return out.reshape(*lead, N)
+    lib = _lib.load()
+    stream = _lib.stream_handle(x.device)
+    need = lib.fi_int4_matmul_workspace_size(M, N, K)
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = _workspace(x.device, stream, need)
+    ws_ptr = workspace.data_ptr() if need else None
+    ws_bytes = workspace.numel() * workspace.element_size() if need else 0
+    rc = lib.fi_int4_matmul(x2.data_ptr(), x2.stride(0), M, K, wt.data_ptr(), w_stride, s_ptr,
+                            s_stride, N, groupsize, out.data_ptr(), out.stride(0), ws_ptr,
+                            ws_bytes, stream)
+    _lib.check(rc, "int4_matmul")
+    return out.reshape(*lead, N)
+
+
+def quantize_int4_groupwise(w: torch.Tensor, groupsize: int = 128
+                            ) -> tuple[torch.Tensor, torch.Tensor]:
+    """loader.py:9-41: fp16 ``w [N, K]`` -> (packed int8 ``[N, K/2]``, scales fp16
+    ``[N, K/groupsize]``), bit-exact with the reference's arithmetic on a CUDA device."""
+    _need_cuda("w", w)
+    if w.dtype != torch.float16 or w.dim() != 2:
+        raise TypeError("w must be a 2-D float16 tensor")
+    N, K = w.shape
+    if K % groupsize:
+        raise ValueError(f"K ({K}) must be multiple of groupsize ({groupsize})")
+    wt = _rows16(w, 2)
+    packed = torch.empty(N, K // 2, dtype=torch.int8, device=w.device)
+    scales = torch.empty(N, K // groupsize, dtype=torch.float16, device=w.device)
+    lib = _lib.load()
+    rc = lib.fi_int4_quantize(wt.data_ptr(), wt.stride(0), N, K, groupsize, packed.data_ptr(),
+                              packed.stride(0), scales.data_ptr(), scales.stride(0),
+                              _lib.stream_handle(w.device))
+    _lib.check(rc, "quantize_int4_groupwise")
+    return packed, scales
+
+
+def dequantize_int4(packed: torch.Tensor, scales: torch.Tensor,
+                    groupsize: int = 128) -> torch.Tensor:
+    """kernels/matmul.py:197-214 (``_dequant_storage``): -> fp16 ``[N, K]``, each weight
+    fp16(q * scale)."""
+    _need_cuda("packed", packed)
+    N, K = packed.shape[0], packed.shape[1] * 2
+    if scales.shape != (N, K // groupsize):
+        raise ValueError(f"scales {tuple(scales.shape)} do not match packed {tuple(packed.shape)}")
+    pk = packed if packed.is_contiguous() else packed.contiguous()
+    sc = scales if scales.is_contiguous() else scales.contiguous()
+    w = torch.empty(N, K, dtype=torch.float16, device=packed.device)
+    lib = _lib.load()
+    rc = lib.fi_int4_dequantize(pk.data_ptr(), pk.stride(0), sc.data_ptr(), sc.stride(0), N, K,
+                                groupsize, w.data_ptr(), w.stride(0),
+                                _lib.stream_handle(packed.device))
+    _lib.check(rc, "dequantize_int4")
+    return w

@@ -7,6 +7,8 @@ what the algorithm must move or compute, independent of how a kernel does it:
   token at 8 kv heads x 128 dims x fp16 x 2), plus q and o, plus the block-table
   entries covering the context;
 * causal prefill — 4 * B * H * S^2 * D / 2 flops (QK^T and PV over the causal half);
+* INT4 linear layer — packed weights (K/2 bytes per row) and fp16 scales (2 bytes per
+  128-group) read once, X read once, the fp16 output written once; 2 * M * N * K flops;
 * fused RoPE + KV write — q, k, v rows read once, the cos/sin rows of the distinct
   positions read once, rotated q (and k when returned) written once, k and v rows
   written into the pool once.
@@ -51,3 +53,12 @@ def rope_store_bytes(batch: int, tokens: int, num_q_heads: int, num_kv_heads: in
     write = n * num_q_heads * row
     write += n * num_kv_heads * row * ((1 if return_k else 0) + (2 if pool else 0))
     return read + write
+
+
+def int4_matmul_bytes(M: int, N: int, K: int, groupsize: int = 128) -> int:
+    """Algorithmic HBM bytes of one INT4 linear-layer call."""
+    return N * K // 2 + N * (K // groupsize) * 2 + M * K * 2 + M * N * 2
+
+
+def matmul_flops(M: int, N: int, K: int) -> float:
+    return 2.0 * M * N * K

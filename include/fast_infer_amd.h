@@ -250,6 +250,48 @@ FI_API int fi_kv_reset(int32_t* block_table, int64_t bt_stride, int64_t max_bloc
                 int32_t* free_queue, int32_t* state, int64_t num_blocks, void* stream);
 
 /*
+ * INT4 group-quantized linear layer, C = X * W^T (kernels/matmul.py:217-231,
+ * int4_matmul; the fused kernel :14-132 for packed weights, the fp16 kernel :135-186
+ * for dequantized ones).
+ *   x      : fp16 [M, K], row stride x_stride elements (16-byte aligned rows).
+ *   w      : with scales: int8 bytes [N, K/2] (loader.py:9-41 packing: byte j of a row holds
+ *            k = 2j in the low nibble, k = 2j+1 in the high nibble, two's complement),
+ *            row stride w_stride bytes (multiple of 16); scales fp16 [N, K/groupsize], row
+ *            stride s_stride elements.  Without scales (NULL): fp16 [N, K], row stride
+ *            w_stride elements.
+ *   out    : fp16 [M, N], row stride out_stride elements.
+ *   Each weight is fp16(q * scale) exactly as the reference dequantizes it; products are
+ *   accumulated in fp32 and rounded to fp16 once.  groupsize must be 128 and K a multiple
+ *   of 128.  Some shapes split K: then a workspace of
+ *   fi_int4_matmul_workspace_size(M, N, K) bytes is required (FI_ERR_WORKSPACE otherwise);
+ *   calls that overlap in time must not share one.
+ */
+FI_API size_t fi_int4_matmul_workspace_size(int64_t M, int64_t N, int64_t K);
+FI_API int fi_int4_matmul(const void* x, int64_t x_stride, int64_t M, int64_t K,
+                   const void* w, int64_t w_stride, const void* scales, int64_t s_stride,
+                   int64_t N, int64_t groupsize, void* out, int64_t out_stride,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * quantize_int4_groupwise (loader.py:9-41) on the device, bit-exact with the reference's
+ * fp16 tensor arithmetic on a CUDA device: amax = max |w| over each 128-wide group,
+ * clamped below at fp16(1e-6); scale = fp16(fp32(amax) * fp32(1/7)); q =
+ * round_half_even(fp16(fp32(w) / fp32(scale))) clamped to [-8, 7], packed two per byte.
+ *   w fp16 [N, K] (row stride w_stride elements, 16-byte aligned rows);
+ *   packed int8 [N, K/2] (row stride p_stride bytes), scales fp16 [N, K/128].
+ */
+FI_API int fi_int4_quantize(const void* w, int64_t w_stride, int64_t N, int64_t K,
+                     int64_t groupsize, void* packed, int64_t p_stride, void* scales,
+                     int64_t s_stride, void* stream);
+
+/*
+ * _dequant_storage (kernels/matmul.py:197-214): w[n, k] = fp16(q[n, k] * scale[n, k/128]).
+ */
+FI_API int fi_int4_dequantize(const void* packed, int64_t p_stride, const void* scales,
+                       int64_t s_stride, int64_t N, int64_t K, int64_t groupsize, void* w,
+                       int64_t w_stride, void* stream);
+
+/*
  * Self-test of the gfx950 MFMA fragment layout the attention kernels assume
  * (no counterpart in the reference; used by the test suite).  One wave computes
  * C[16x16] = A[16x32] * B[32x16] with v_mfma_f32_16x16x32_f16, where lane l holds

@@ -15,6 +15,10 @@ Contents (each function cites the reference file:line it restates):
 * ``rope`` — numpy restatement of the RoPE table and of its fp16 application
   (kernels/rope.py:9-44), and of RoPE followed by the pool write (model.py:101,
   :117, :120).
+* ``block_manager`` — the reference allocator driven with per-row token counts, plus
+  row release (the device block manager's checker).
+* ``int4`` — numpy restatement of the INT4 weight format: quantize (loader.py:9-41),
+  unpack / dequantize (matmul.py:197-214), and the float64 product with its error bound.
 * ``ref_algo.c`` (+ ``native``) — the same tile algorithms in C with OpenMP, used
   as the CPU baseline ("port").
 

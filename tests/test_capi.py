@@ -34,6 +34,8 @@ def test_header_declares_entry_points():
     names = _declared()
     for n in ("fi_flash_attention_fwd", "fi_paged_attention_fwd", "fi_kv_store",
               "fi_rope_store_kv", "fi_kv_append", "fi_kv_release", "fi_kv_reset",
+              "fi_int4_matmul", "fi_int4_matmul_workspace_size", "fi_int4_quantize",
+              "fi_int4_dequantize",
               "fi_paged_attention_workspace_size", "fi_last_error", "fi_version"):
         assert n in names
 
@@ -151,6 +153,34 @@ def test_block_manager_validation(lib):
     # empty batches return before any launch
     assert lib.fi_kv_append(*st, 8, 16, 0, None, 1, None, None, None) == _lib.FI_OK
     assert lib.fi_kv_release(*st, 8, 0, None, None) == _lib.FI_OK
+
+
+def test_int4_validation(lib):
+    from fast_infer_amd import _lib
+
+    # groupsize other than 128, K not a multiple of 128, misaligned rows, null pointers
+    assert lib.fi_int4_matmul(16, 256, 1, 256, 16, 128, 16, 2, 64, 64, 16, 64, None, 0,
+                              None) == _lib.FI_ERR_UNSUPPORTED
+    assert b"groupsize 64" in lib.fi_last_error()
+    assert lib.fi_int4_matmul(16, 200, 1, 200, 16, 112, 16, 2, 64, 128, 16, 64, None, 0,
+                              None) == _lib.FI_ERR_UNSUPPORTED
+    assert lib.fi_int4_matmul(18, 256, 1, 256, 16, 128, 16, 2, 64, 128, 16, 64, None, 0,
+                              None) == _lib.FI_ERR_INVALID
+    assert lib.fi_int4_matmul(None, 256, 1, 256, 16, 128, 16, 2, 64, 128, 16, 64, None, 0,
+                              None) == _lib.FI_ERR_INVALID
+    # a split call without its workspace is rejected before launch
+    need = lib.fi_int4_matmul_workspace_size(40, 5120, 3072)
+    assert need > 0
+    assert lib.fi_int4_matmul(16, 3072, 40, 3072, 16, 1536, 16, 24, 5120, 128, 16, 5120, None,
+                              0, None) == _lib.FI_ERR_WORKSPACE
+    assert lib.fi_int4_quantize(16, 256, 4, 256, 64, 16, 128, 16, 2, None) == \
+        _lib.FI_ERR_UNSUPPORTED
+    assert lib.fi_int4_dequantize(16, 128, 16, 2, 4, 100, 128, 16, 256, None) == \
+        _lib.FI_ERR_INVALID
+    # empty calls return before any launch
+    assert lib.fi_int4_matmul(16, 256, 0, 256, 16, 128, 16, 2, 64, 128, 16, 64, None, 0,
+                              None) == _lib.FI_OK
+    assert lib.fi_int4_quantize(16, 256, 0, 256, 128, 16, 128, 16, 2, None) == _lib.FI_OK
 
 
 def test_workspace_size(lib):

@@ -1,0 +1,138 @@
+"""GPU parity tests of the INT4 linear layer (``fi_int4_quantize`` / ``fi_int4_dequantize`` /
+``fi_int4_matmul``), marked ``gpu``.
+
+* quantize and dequantize bit-exact against the oracle (oracle/int4.py), including
+  all-zero groups, subnormal scales and values near the top of fp16;
+* int4_matmul with packed weights within the fp32-accumulation bound of the float64
+  product on the dequantized weights, for decode-sized M (1..64, split-K) and prefill
+  sizes, odd N, strided X; the speed mode (dequantized fp16 weights) within the same
+  bound, and equal bit for bit where both run the same tiled kernel (prefill sizes).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import banner
+from oracle import int4 as OI
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def _weights(seed, N, K, scale=0.05, big=False):
+    """Random weights with an all-zero group and a tiny group (subnormal scales); with
+    ``big`` also a group near the top of fp16 (products would overflow a matmul)."""
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal((N, K)) * scale).astype(np.float32)
+    w[0, :128] = 0.0
+    w[1 % N, 128 % K:256 % K or K] *= 1e-4
+    if big:
+        w[2 % N, :128] = 3.0e4 * np.sign(w[2 % N, :128])
+    return w.astype(np.float16)
+
+
+@pytest.mark.parametrize("N,K", [(5120, 3072), (3, 256), (130, 8192)])
+def test_quantize_dequantize_bitexact(hip, N, K):
+    banner(f"int4 quantize/dequantize N={N} K={K}")
+    from fast_infer_amd import dequantize_int4, quantize_int4_groupwise
+
+    w = _weights(N + K, N, K, big=True)
+    packed, scales = quantize_int4_groupwise(torch.from_numpy(w).to(DEV))
+    ep, es = OI.quantize_int4_groupwise(w)
+    torch.cuda.synchronize()
+    assert np.array_equal(packed.cpu().numpy(), ep)
+    assert np.array_equal(scales.cpu().numpy().view(np.uint16), es.view(np.uint16))
+    deq = dequantize_int4(packed, scales)
+    ed = OI.dequantize(ep, es)
+    torch.cuda.synchronize()
+    assert np.array_equal(deq.cpu().numpy().view(np.uint16), ed.view(np.uint16))
+
+
+def _check(out, x, w16):
+    got = out.float().cpu().numpy().astype(np.float64)
+    exact = OI.matmul_exact(x, w16)
+    bound = OI.matmul_bound(x, w16)
+    assert np.all(np.abs(got - exact) <= bound), float(np.max(np.abs(got - exact) - bound))
+
+
+@pytest.mark.parametrize("M", [1, 5, 16, 17, 33, 64, 100, 300])
+@pytest.mark.parametrize("N,K", [(5120, 3072), (3072, 3072), (130, 1024)])
+def test_int4_matmul_vs_oracle(hip, M, N, K):
+    banner(f"int4_matmul M={M} N={N} K={K}")
+    from fast_infer_amd import dequantize_int4, int4_matmul, quantize_int4_groupwise
+
+    w = _weights(7, N, K, 0.02)
+    packed, scales = quantize_int4_groupwise(torch.from_numpy(w).to(DEV))
+    g = torch.Generator().manual_seed(M * 7 + N)
+    x = torch.randn(M, K, generator=g).half()
+    out = int4_matmul(x.to(DEV), (packed, scales))
+    w16 = dequantize_int4(packed, scales)
+    out16 = int4_matmul(x.to(DEV), w16)
+    torch.cuda.synchronize()
+    _check(out, x.numpy(), w16.cpu().numpy())      # memory mode (packed weights)
+    _check(out16, x.numpy(), w16.cpu().numpy())    # speed mode (dequantized weights)
+
+
+def test_int4_matmul_strided_x_and_batch_dims(hip):
+    banner("int4_matmul strided x, [B, S, K] input")
+    from fast_infer_amd import dequantize_int4, int4_matmul, quantize_int4_groupwise
+
+    N, K = 640, 3072
+    w = _weights(8, N, K, 0.02)
+    packed, scales = quantize_int4_groupwise(torch.from_numpy(w).to(DEV))
+    g = torch.Generator().manual_seed(9)
+    big = torch.randn(2, 7, K + 256, generator=g).half()
+    x = big[..., 128:128 + K]                 # [2, 7, K], row stride K + 256
+    out = int4_matmul(x.to(DEV), (packed, scales))
+    assert out.shape == (2, 7, N)
+    torch.cuda.synchronize()
+    _check(out.reshape(14, N), x.reshape(14, K).numpy(), dequantize_int4(packed, scales).cpu().numpy())
+
+
+def test_int4_matmul_prefill_size_sampled(hip):
+    """4 x 512 tokens through the fused QKV weight (N 5120, K 3072): sampled rows against
+    float64, every row equal to the speed-mode result."""
+    banner("int4_matmul M=2048 N=5120 K=3072")
+    from fast_infer_amd import dequantize_int4, int4_matmul, quantize_int4_groupwise
+
+    M, N, K = 2048, 5120, 3072
+    w = _weights(10, N, K, 0.02)
+    packed, scales = quantize_int4_groupwise(torch.from_numpy(w).to(DEV))
+    g = torch.Generator(device=DEV).manual_seed(11)
+    x = torch.randn(M, K, device=DEV, generator=g).half()
+    out = int4_matmul(x, (packed, scales))
+    w16 = dequantize_int4(packed, scales)
+    assert torch.equal(out, int4_matmul(x, w16))   # same tiled kernel: same bits
+    rows = torch.tensor([0, 1, 127, 128, 1000, 2047])
+    _check(out[rows.to(DEV)], x[rows.to(DEV)].cpu().numpy(), w16.cpu().numpy())
+
+
+def test_int4_matmul_workspace(hip):
+    """A split-K call (dequantized weights, 40 rows) with a caller workspace: the same
+    bits as with the cached one, one workspace reused across shapes, and too small a
+    workspace rejected before launch."""
+    banner("int4_matmul workspace")
+    from fast_infer_amd import _lib, dequantize_int4, int4_matmul, quantize_int4_groupwise
+
+    lib = _lib.load()
+    N, K = 5120, 3072
+    M = 40
+    need = lib.fi_int4_matmul_workspace_size(M, N, K)
+    assert need > 0 and lib.fi_int4_matmul_workspace_size(4096, N, K) == 0
+    w = _weights(12, N, K, 0.02)
+    packed, scales = quantize_int4_groupwise(torch.from_numpy(w).to(DEV))
+    w16 = dequantize_int4(packed, scales)
+    x = torch.randn(64, K, device=DEV).half()
+    ws = torch.empty(max(lib.fi_int4_matmul_workspace_size(m, N, K) for m in (17, 40, 64)),
+                     dtype=torch.uint8, device=DEV)
+    for m in (40, 17, 64, 40):
+        a = int4_matmul(x[:m], w16, workspace=ws)
+        b = int4_matmul(x[:m], w16)
+        assert torch.equal(a, b)
+    out = torch.empty(M, N, dtype=torch.float16, device=DEV)
+    rc = lib.fi_int4_matmul(x.data_ptr(), K, M, K, w16.data_ptr(), K, None, 0, N, 128,
+                            out.data_ptr(), N, ws.data_ptr(), need - 16,
+                            _lib.stream_handle(torch.device(DEV)))
+    assert rc == _lib.FI_ERR_WORKSPACE
