@@ -14,7 +14,8 @@ serve them.  The same line carries:
 * ``decode_step_28layer_b64_paged`` — the same step with the device block manager (one
   append per step) and the fused RoPE + pool write per layer before attention;
 * ``int4_linear`` — the INT4 QKV / O projections around attention (decode batch 64 and 1
-  over 28 layers of weights, GB/s; prefill QKV at 16384 tokens, TFLOP/s);
+  over 28 layers of weights, GB/s; prefill QKV at 16384 tokens, TFLOP/s), RMSNorm fused
+  into the QKV projection against the two-step form, and RMSNorm alone at 16384 rows;
 * ``rope_store_kv`` — the fused RoPE + K/V pool write (batch 4 x 4096 prefill, batch 64
   decode), GB/s of algorithmic traffic;
 * ``decode_28layer_b64`` — a 28-layer decode step over per-layer pools, batch 64,
@@ -309,8 +310,27 @@ def bench_int4(torch, fi, timer, steps, warmup, dev):
         t = timer.run(step, max(1, steps // 10), max(1, warmup // 5))
         nbytes = L * (R.int4_matmul_bytes(M, NQKV, K) + R.int4_matmul_bytes(M, NO, K))
         res[f"decode_b{M}"] = dict(t=t, bytes=nbytes, gbs=nbytes / t / 1e9)
+    # RMSNorm (model.py:82) fused with the QKV projection against the two-step form
+    nws = [(torch.randn(K, device=dev, generator=g) * 0.1 + 1).half() for _ in range(L)]
+    for M in (1, 64):
+        x = torch.randn(M, K, device=dev, generator=g).half()
+
+        def fused():
+            for (wqkv, _), nw in zip(layers, nws):
+                fi.rms_norm_int4_matmul(x, nw, wqkv)
+
+        def two_step():
+            for (wqkv, _), nw in zip(layers, nws):
+                fi.int4_matmul(fi.rms_norm(x, nw), wqkv)
+
+        res[f"norm_qkv_b{M}"] = dict(
+            fused=timer.run(fused, max(1, steps // 10), max(1, warmup // 5)) / L,
+            two_step=timer.run(two_step, max(1, steps // 10), max(1, warmup // 5)) / L)
     M = 4 * 4096
     x = torch.randn(M, K, device=dev, generator=g).half()
+    t = timer.run(lambda: fi.rms_norm(x, nws[0]), steps, warmup)
+    nbytes = 2 * M * K * 2 + K * 2
+    res["rms_norm_prefill"] = dict(t=t, bytes=nbytes, gbs=nbytes / t / 1e9)
     wqkv = layers[0][0]
     t = timer.run(lambda: fi.int4_matmul(x, wqkv), max(1, steps // 10), max(1, warmup // 5))
     fl = R.matmul_flops(M, NQKV, K)
@@ -510,10 +530,22 @@ def main():
                           "frac_hbm": round(d1["gbs"] / R.HBM_PEAK_GBS, 4)},
             "prefill_qkv_m16384": {"us_per_call": round(pq["t"] * 1e6, 1),
                                    "TFLOP/s": round(pq["tflops"], 1),
-                                   "frac_mfma": round(pq["tflops"] / R.FP16_MFMA_PEAK_TFLOPS, 4)}}
+                                   "frac_mfma": round(pq["tflops"] / R.FP16_MFMA_PEAK_TFLOPS, 4)},
+            "rms_norm_qkv": {f"b{M}": {"fused_us": round(q[f"norm_qkv_b{M}"]["fused"] * 1e6, 2),
+                                       "two_step_us": round(q[f"norm_qkv_b{M}"]["two_step"] * 1e6,
+                                                            2)}
+                             for M in (1, 64)},
+            "rms_norm_m16384": {"us_per_call": round(q["rms_norm_prefill"]["t"] * 1e6, 2),
+                                "GB/s": round(q["rms_norm_prefill"]["gbs"], 1),
+                                "frac_hbm": round(q["rms_norm_prefill"]["gbs"] / R.HBM_PEAK_GBS,
+                                                  4)}}
         print(f"[bench] int4 decode b64 {d64['t'] / 28 * 1e6:.2f} us/layer {d64['gbs']:.0f} GB/s; "
               f"b1 {d1['t'] / 28 * 1e6:.2f} us/layer {d1['gbs']:.0f} GB/s; prefill qkv "
               f"{pq['t'] * 1e6:.0f} us {pq['tflops']:.0f} TFLOP/s", file=sys.stderr, flush=True)
+        print("[bench] norm+qkv fused/two-step us: " + ", ".join(
+            f"b{M} {q[f'norm_qkv_b{M}']['fused'] * 1e6:.2f}/{q[f'norm_qkv_b{M}']['two_step'] * 1e6:.2f}"
+            for M in (1, 64)) + f"; rms_norm 16384x3072 {q['rms_norm_prefill']['t'] * 1e6:.1f} us "
+            f"{q['rms_norm_prefill']['gbs']:.0f} GB/s", file=sys.stderr, flush=True)
 
     if not a.no_cpu_baseline:
         if dec is not None:

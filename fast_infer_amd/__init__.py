@@ -13,7 +13,8 @@ from .attention import flash_attention, paged_attention, paged_attention_workspa
 from .kv_cache import KVCache
 from .kv_store import (allocate_decode, allocate_prefill, store_kv, store_kv_decode,
                        store_kv_prefill)
-from .matmul import dequantize_int4, int4_matmul, quantize_int4_groupwise
+from .matmul import (dequantize_int4, int4_matmul, quantize_int4_groupwise, rms_norm,
+                     rms_norm_int4_matmul)
 from .paged_cache import PagedKVCache
 from .rope import (apply_rope, precompute_freqs, rope_store_kv, rope_store_kv_decode,
                    rope_store_kv_prefill)
@@ -27,6 +28,8 @@ __all__ = [
     "int4_matmul",
     "quantize_int4_groupwise",
     "dequantize_int4",
+    "rms_norm",
+    "rms_norm_int4_matmul",
     "store_kv",
     "store_kv_prefill",
     "store_kv_decode",

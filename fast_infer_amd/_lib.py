@@ -116,6 +116,18 @@ SIGNATURES = {
     "fi_int4_dequantize": (
         ctypes.c_int, [_ptr, _i64, _ptr, _i64, _i64, _i64, _i64, _ptr, _i64, _ptr],
     ),
+    "fi_rmsnorm": (ctypes.c_int, [_ptr, _i64, _i64, _i64, _ptr, _f32, _ptr, _i64, _ptr]),
+    "fi_rmsnorm_int4_matmul_workspace_size": (_sz, [_i64, _i64, _i64]),
+    "fi_rmsnorm_int4_matmul": (
+        ctypes.c_int,
+        [_ptr, _i64, _i64, _i64,                 # x, stride, M, K
+         _ptr, _f32,                             # norm weight, eps
+         _ptr, _i64, _ptr, _i64,                 # w, stride, scales, stride
+         _i64, _i64,                             # N, groupsize
+         _ptr, _i64,                             # out, stride
+         _ptr, _sz,                              # workspace
+         _ptr],                                  # stream
+    ),
     "fi_selftest_mfma_f16": (ctypes.c_int, [_ptr, _ptr, _ptr, _ptr]),
 }
 

@@ -44,6 +44,8 @@ struct Params {
   int64_t out_stride;
   float* partial;    // [splits, M, N] fp32 when splits > 1
   int groups_per_split;
+  const half_t* norm_w;  // RMSNorm weight [K] when the norm is fused into the X operand
+  float eps;
 };
 
 __device__ __forceinline__ uint32_t as_u32(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
@@ -102,6 +104,116 @@ __device__ __forceinline__ void store_tile(const Params& p, const floatx4 (&acc)
       }
     }
   }
+}
+
+// ---------------------------------------------------------------------------------------
+// RMSNorm (kernels/rms_norm.py:8-43): y = fp16((x * r) * w) with r = rsqrt(sum(x^2)/K + eps),
+// all in fp32.  One wave reduces one row.
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+  return v;
+}
+
+// Rows up to kRowChunks * 512 elements are held in registers (16 bytes per lane per 512
+// elements), every load issued before the first use; longer rows loop.
+constexpr int kRowChunks = 16;
+
+__device__ __forceinline__ float sum_sq8(u32x4 v) {
+  const half8 h = as_half8(v);
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s += (float)h[e] * (float)h[e];
+  return s;
+}
+
+// r of one row of K (a multiple of 8) elements, computed by the calling wave
+__device__ __forceinline__ float row_rsqrt(const half_t* xrow, int K, float eps, int lane) {
+  float s = 0.f;
+  if (K <= kRowChunks * 512) {
+    u32x4 v[kRowChunks];
+#pragma unroll
+    for (int i = 0; i < kRowChunks; ++i) {
+      const int k = lane * 8 + i * 512;
+      v[i] = k < K ? *(const u32x4*)(xrow + k) : u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int i = 0; i < kRowChunks; ++i) s += sum_sq8(v[i]);
+  } else {
+    for (int k = lane * 8; k < K; k += 512) s += sum_sq8(*(const u32x4*)(xrow + k));
+  }
+  s = wave_sum(s);
+  return rsqrtf(s / (float)K + eps);
+}
+
+// eight normalized elements: fp16((x * r) * w), products rounded separately (no fma)
+__device__ __forceinline__ u32x4 norm8(u32x4 xv, float r, u32x4 wv) {
+#pragma clang fp contract(off)
+  const half8 x = as_half8(xv);
+  const half8 w = as_half8(wv);
+  half8 y;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) y[e] = (half_t)(((float)x[e] * r) * (float)w[e]);
+  return as_u32x4(y);
+}
+
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const half_t* x, int64_t x_stride, int M,
+                                                      int K, const half_t* w, float eps,
+                                                      half_t* out, int64_t out_stride) {
+  const int lane = threadIdx.x & 63;
+  const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (m >= M) return;
+  const half_t* xr = x + (int64_t)m * x_stride;
+  half_t* o = out + (int64_t)m * out_stride;
+  if (K <= kRowChunks * 512) {  // the row is read once, into registers
+    u32x4 v[kRowChunks], wv[kRowChunks];
+#pragma unroll
+    for (int i = 0; i < kRowChunks; ++i) {
+      const int k = lane * 8 + i * 512;
+      v[i] = k < K ? *(const u32x4*)(xr + k) : u32x4{0, 0, 0, 0};
+      wv[i] = k < K ? *(const u32x4*)(w + k) : u32x4{0, 0, 0, 0};
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < kRowChunks; ++i) s += sum_sq8(v[i]);
+    const float r = rsqrtf(wave_sum(s) / (float)K + eps);
+#pragma unroll
+    for (int i = 0; i < kRowChunks; ++i) {
+      const int k = lane * 8 + i * 512;
+      if (k < K) *(u32x4*)(o + k) = norm8(v[i], r, wv[i]);
+    }
+    return;
+  }
+  const float r = row_rsqrt(xr, K, eps, lane);
+  for (int k = lane * 8; k < K; k += 512)
+    *(u32x4*)(o + k) = norm8(*(const u32x4*)(xr + k), r, *(const u32x4*)(w + k));
+}
+
+// One row normalized by the calling wave into dst (LDS or global), K a multiple of 8.
+__device__ __forceinline__ void norm_row_to(const half_t* xr, const half_t* w, int K, float eps,
+                                            half_t* dst, int lane) {
+  if (K <= kRowChunks * 512) {
+    u32x4 v[kRowChunks];
+#pragma unroll
+    for (int i = 0; i < kRowChunks; ++i) {
+      const int k = lane * 8 + i * 512;
+      v[i] = k < K ? *(const u32x4*)(xr + k) : u32x4{0, 0, 0, 0};
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < kRowChunks; ++i) s += sum_sq8(v[i]);
+    const float r = rsqrtf(wave_sum(s) / (float)K + eps);
+#pragma unroll
+    for (int i = 0; i < kRowChunks; ++i) {
+      const int k = lane * 8 + i * 512;
+      if (k < K) *(u32x4*)(dst + k) = norm8(v[i], r, *(const u32x4*)(w + k));
+    }
+    return;
+  }
+  const float r = row_rsqrt(xr, K, eps, lane);
+  for (int k = lane * 8; k < K; k += 512)
+    *(u32x4*)(dst + k) = norm8(*(const u32x4*)(xr + k), r, *(const u32x4*)(w + k));
 }
 
 template <int MT, bool kInt4>
@@ -201,7 +313,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(Params p) {
 // once (16 weight bytes, the scale, and 64 bytes of its X row per group) before any math,
 // so one memory latency covers the chunk; the four waves' sums are added through LDS in
 // a fixed order.
-template <bool kInt4, int kChunk>
+template <bool kInt4, int kChunk, bool kNorm>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(Params p) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -216,6 +328,17 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(Params p) {
   // columns of rows past M are never stored
   const int mc = m_ok ? m : p.M - 1;
   const int groups = p.K / kGroup;
+  // fused norm: the workgroup's (at most 16, in practice a few) rows are normalized once
+  // into LDS, [rows, K] fp16, and the X operand is read from there
+  extern __shared__ __attribute__((aligned(16))) half_t xn[];
+  const int rows_n = min(16, p.M - (int)blockIdx.y * 16);
+  if constexpr (kNorm) {
+    for (int r = wave; r < rows_n; r += 4)
+      norm_row_to(p.x + (int64_t)(blockIdx.y * 16 + r) * p.x_stride, p.norm_w, p.K, p.eps,
+                  xn + r * p.K, lane);
+    __syncthreads();
+  }
+  const half_t* xrow_n = xn + min(row, rows_n - 1) * p.K;
 
   floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
   for (int g0 = wave; g0 < groups; g0 += 4 * kChunk) {
@@ -223,7 +346,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(Params p) {
     // the end reload the last group and are skipped below), so one latency covers them
     u32x4 wv[kInt4 ? kChunk : 4 * kChunk];
     half_t sv[kChunk];
-    u32x4 xv[4 * kChunk];
+    u32x4 xv[kNorm ? 1 : 4 * kChunk];
 #pragma unroll
     for (int c = 0; c < kChunk; ++c) {
       const int g = min(g0 + 4 * c, groups - 1);
@@ -235,9 +358,11 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(Params p) {
 #pragma unroll
         for (int s = 0; s < 4; ++s) wv[4 * c + s] = *(const u32x4*)(wr + 8 * s);
       }
-      const half_t* xr = p.x + (int64_t)mc * p.x_stride + g * kGroup + grp * 32;
+      if constexpr (!kNorm) {
+        const half_t* xr = p.x + (int64_t)mc * p.x_stride + g * kGroup + grp * 32;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) xv[4 * c + s] = *(const u32x4*)(xr + 8 * s);
+        for (int s = 0; s < 4; ++s) xv[4 * c + s] = *(const u32x4*)(xr + 8 * s);
+      }
     }
 #pragma unroll
     for (int c = 0; c < kChunk; ++c) {
@@ -249,7 +374,12 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(Params p) {
             wf = dequant8(wv[c][s], half2_t{sv[c], sv[c]});
           else
             wf = as_half8(wv[4 * c + s]);
-          acc = mfma16x16x32(wf, as_half8(xv[4 * c + s]), acc);
+          u32x4 xf;
+          if constexpr (kNorm)
+            xf = *(const u32x4*)(xrow_n + (g0 + 4 * c) * kGroup + grp * 32 + 8 * s);
+          else
+            xf = xv[4 * c + s];
+          acc = mfma16x16x32(wf, as_half8(xf), acc);
         }
       }
     }
@@ -406,35 +536,36 @@ extern "C" size_t fi_int4_matmul_workspace_size(int64_t M, int64_t N, int64_t K)
   return pl.splits > 1 ? (size_t)pl.splits * M * N * sizeof(float) : 0;
 }
 
-extern "C" int fi_int4_matmul(const void* x, int64_t x_stride, int64_t M, int64_t K,
-                              const void* w, int64_t w_stride, const void* scales,
-                              int64_t s_stride, int64_t N, int64_t groupsize, void* out,
-                              int64_t out_stride, void* workspace, size_t workspace_bytes,
-                              void* stream) {
+namespace {
+
+using fi::half_t;
+
+// Shared validation for the linear-layer entry points; FI_OK when the operands are usable.
+int check_linear(const char* fn, const void* x, int64_t x_stride, int64_t M, int64_t K,
+                 const void* w, int64_t w_stride, const void* scales, int64_t s_stride,
+                 int64_t N, int64_t groupsize, const void* out, int64_t out_stride) {
   using namespace fi;
   using namespace fi::gemm;
-  clear_error();
   if (M < 0 || N < 0 || K < 0) {
-    set_error("fi_int4_matmul: negative size");
+    set_error("%s: negative size", fn);
     return FI_ERR_INVALID;
   }
   if (M == 0 || N == 0) return FI_OK;
   const bool int4 = scales != nullptr;
   if (int4 && groupsize != kGroup) {
-    set_error("fi_int4_matmul: groupsize %lld not supported (only %d)", (long long)groupsize,
-              kGroup);
+    set_error("%s: groupsize %lld not supported (only %d)", fn, (long long)groupsize, kGroup);
     return FI_ERR_UNSUPPORTED;
   }
   if (K == 0 || K % kGroup) {
-    set_error("fi_int4_matmul: K %lld must be a positive multiple of %d", (long long)K, kGroup);
+    set_error("%s: K %lld must be a positive multiple of %d", fn, (long long)K, kGroup);
     return FI_ERR_UNSUPPORTED;
   }
   if (M >= (1ll << 30) || N >= (1ll << 30) || K >= (1ll << 30)) {
-    set_error("fi_int4_matmul: sizes too large");
+    set_error("%s: sizes too large", fn);
     return FI_ERR_UNSUPPORTED;
   }
   if (!x || !w || !out) {
-    set_error("fi_int4_matmul: null pointer");
+    set_error("%s: null pointer", fn);
     return FI_ERR_INVALID;
   }
   const bool x_ok = ((uintptr_t)x & 15) == 0 && x_stride % 8 == 0 && x_stride >= K;
@@ -442,42 +573,62 @@ extern "C" int fi_int4_matmul(const void* x, int64_t x_stride, int64_t M, int64_
                             ((uintptr_t)scales & 1) == 0 && s_stride >= K / kGroup)
                          : (((uintptr_t)w & 15) == 0 && w_stride % 8 == 0 && w_stride >= K);
   if (!x_ok || !w_ok || ((uintptr_t)out & 1) || out_stride < N) {
-    set_error("fi_int4_matmul: rows must be 16-byte aligned and strides cover the rows "
-              "(x_stride %lld, w_stride %lld, out_stride %lld)", (long long)x_stride,
+    set_error("%s: rows must be 16-byte aligned and strides cover the rows "
+              "(x_stride %lld, w_stride %lld, out_stride %lld)", fn, (long long)x_stride,
               (long long)w_stride, (long long)out_stride);
     return FI_ERR_INVALID;
   }
-  const Plan pl = plan(M, N, K);
-  hipStream_t st = (hipStream_t)stream;
-  if (pl.gemv_rows) {
-    Params p;
-    p.x = (const half_t*)x;
-    p.x_stride = x_stride;
-    p.M = (int)M;
-    p.K = (int)K;
-    p.N = (int)N;
-    p.w = (const uint8_t*)w;
-    p.w_stride = w_stride;
-    p.scales = (const half_t*)scales;
-    p.s_stride = s_stride;
-    p.out = (half_t*)out;
-    p.out_stride = out_stride;
+  return FI_OK;
+}
+
+// kNorm: the RMSNorm is fused into the decode kernel (only on the gemv path).
+template <bool kNorm>
+void launch_linear(const fi::gemm::Params& base, bool int4, const fi::gemm::Plan& pl,
+                   void* workspace, hipStream_t st) {
+  using namespace fi::gemm;
+  Params p = base;
+  if (kNorm || pl.gemv_rows) {
     p.partial = nullptr;
-    p.groups_per_split = (int)(K / kGroup);
-    const dim3 grid((unsigned)((N + 15) / 16), (unsigned)((M + 15) / 16), 1);
+    p.groups_per_split = p.K / kGroup;
+    const dim3 grid((unsigned)((p.N + 15) / 16), (unsigned)((p.M + 15) / 16), 1);
+    const size_t lds = kNorm ? (size_t)std::min(p.M, 16) * p.K * sizeof(half_t) : 0;
     if (int4)
-      hipLaunchKernelGGL((gemv_kernel<true, 6>), grid, dim3(kThreads), 0, st, p);
+      hipLaunchKernelGGL((gemv_kernel<true, 6, kNorm>), grid, dim3(kThreads), lds, st, p);
     else
-      hipLaunchKernelGGL((gemv_kernel<false, 3>), grid, dim3(kThreads), 0, st, p);
-    return check_launch("fi_int4_matmul");
+      hipLaunchKernelGGL((gemv_kernel<false, 3, kNorm>), grid, dim3(kThreads), lds, st, p);
+    return;
   }
-  const size_t need = pl.splits > 1 ? (size_t)pl.splits * M * N * sizeof(float) : 0;
-  if (need && (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 15))) {
-    set_error("fi_int4_matmul: workspace of %zu bytes needed (have %zu)", need,
-              workspace ? workspace_bytes : (size_t)0);
-    return FI_ERR_WORKSPACE;
+  p.partial = pl.splits > 1 ? (float*)workspace : nullptr;
+  const int groups = p.K / kGroup;
+  p.groups_per_split = (groups + pl.splits - 1) / pl.splits;
+  const dim3 grid((unsigned)((p.N + kNTile - 1) / kNTile), (unsigned)((p.M + pl.mt - 1) / pl.mt),
+                  (unsigned)pl.splits);
+#define FI_GEMM_LAUNCH(MT)                                                                    \
+  do {                                                                                      \
+    if (int4)                                                                               \
+      hipLaunchKernelGGL((gemm_kernel<MT, true>), grid, dim3(kThreads), 0, st, p);           \
+    else                                                                                    \
+      hipLaunchKernelGGL((gemm_kernel<MT, false>), grid, dim3(kThreads), 0, st, p);          \
+  } while (0)
+  switch (pl.mt) {
+    case 16: FI_GEMM_LAUNCH(16); break;
+    case 32: FI_GEMM_LAUNCH(32); break;
+    case 64: FI_GEMM_LAUNCH(64); break;
+    default: FI_GEMM_LAUNCH(128); break;
   }
-  Params p;
+#undef FI_GEMM_LAUNCH
+  if (pl.splits > 1) {
+    const int64_t total = (int64_t)p.M * p.N;
+    const int64_t blocks = std::min<int64_t>((total + 255) / 256, 4096);
+    hipLaunchKernelGGL(reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
+                       (const float*)workspace, pl.splits, p.M, p.N, p.out, p.out_stride);
+  }
+}
+
+fi::gemm::Params make_params(const void* x, int64_t x_stride, int64_t M, int64_t K,
+                             const void* w, int64_t w_stride, const void* scales,
+                             int64_t s_stride, int64_t N, void* out, int64_t out_stride) {
+  fi::gemm::Params p;
   p.x = (const half_t*)x;
   p.x_stride = x_stride;
   p.M = (int)M;
@@ -489,39 +640,140 @@ extern "C" int fi_int4_matmul(const void* x, int64_t x_stride, int64_t M, int64_
   p.s_stride = s_stride;
   p.out = (half_t*)out;
   p.out_stride = out_stride;
-  p.partial = pl.splits > 1 ? (float*)workspace : nullptr;
-  const int groups = (int)(K / kGroup);
-  p.groups_per_split = (groups + pl.splits - 1) / pl.splits;
-  const dim3 grid((unsigned)((N + kNTile - 1) / kNTile), (unsigned)((M + pl.mt - 1) / pl.mt),
-                  (unsigned)pl.splits);
-  if (grid.y > 65535) {
+  p.partial = nullptr;
+  p.groups_per_split = 0;
+  p.norm_w = nullptr;
+  p.eps = 0.f;
+  return p;
+}
+
+size_t split_bytes(int64_t M, int64_t N, const fi::gemm::Plan& pl) {
+  return pl.splits > 1 ? (size_t)pl.splits * M * N * sizeof(float) : 0;
+}
+
+// The norm is fused into the decode kernel for a few rows (each workgroup normalizes them
+// into LDS once); otherwise a separate RMSNorm pass writes the normalized rows into the
+// workspace first (every column tile would re-read and re-normalize its rows).
+bool fuse_norm(int64_t M, int64_t K, const fi::gemm::Plan& pl) {
+  static const int max_m = fi::gemm::env_int("FI_RMSNORM_FUSE_MAX_M", 4);
+  // the decode kernel keeps its normalized rows in LDS: at most 64 KB of them
+  return pl.gemv_rows && M <= max_m && std::min<int64_t>(M, 16) * K * 2 <= 65536;
+}
+
+size_t norm_rows_bytes(int64_t M, int64_t K) { return (size_t)((M * K * 2 + 255) / 256 * 256); }
+
+}  // namespace
+
+extern "C" int fi_int4_matmul(const void* x, int64_t x_stride, int64_t M, int64_t K,
+                              const void* w, int64_t w_stride, const void* scales,
+                              int64_t s_stride, int64_t N, int64_t groupsize, void* out,
+                              int64_t out_stride, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+  using namespace fi;
+  using namespace fi::gemm;
+  clear_error();
+  int rc = check_linear("fi_int4_matmul", x, x_stride, M, K, w, w_stride, scales, s_stride, N,
+                        groupsize, out, out_stride);
+  if (rc != FI_OK || M == 0 || N == 0) return rc;
+  const Plan pl = plan(M, N, K);
+  const size_t need = split_bytes(M, N, pl);
+  if (need && (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 15))) {
+    set_error("fi_int4_matmul: workspace of %zu bytes needed (have %zu)", need,
+              workspace ? workspace_bytes : (size_t)0);
+    return FI_ERR_WORKSPACE;
+  }
+  if ((M + pl.mt - 1) / pl.mt > 65535) {
     set_error("fi_int4_matmul: M %lld too large", (long long)M);
     return FI_ERR_UNSUPPORTED;
   }
-#define FI_GEMM_LAUNCH(MT)                                                                \
-  do {                                                                                  \
-    if (int4)                                                                           \
-      hipLaunchKernelGGL((gemm_kernel<MT, true>), grid, dim3(kThreads), 0, st, p);       \
-    else                                                                                \
-      hipLaunchKernelGGL((gemm_kernel<MT, false>), grid, dim3(kThreads), 0, st, p);      \
-  } while (0)
-  {
-    switch (pl.mt) {
-      case 16: FI_GEMM_LAUNCH(16); break;
-      case 32: FI_GEMM_LAUNCH(32); break;
-      case 64: FI_GEMM_LAUNCH(64); break;
-      default: FI_GEMM_LAUNCH(128); break;
-    }
-  }
-#undef FI_GEMM_LAUNCH
-  if (pl.splits > 1) {
-    const int64_t total = M * N;
-    const int64_t blocks = std::min<int64_t>((total + 255) / 256, 4096);
-    hipLaunchKernelGGL(reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
-                       (const float*)workspace, pl.splits, (int)M, (int)N, (half_t*)out,
-                       out_stride);
-  }
+  launch_linear<false>(make_params(x, x_stride, M, K, w, w_stride, scales, s_stride, N, out,
+                                   out_stride),
+                       scales != nullptr, pl, workspace, (hipStream_t)stream);
   return check_launch("fi_int4_matmul");
+}
+
+extern "C" size_t fi_rmsnorm_int4_matmul_workspace_size(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % fi::gemm::kGroup) return 0;
+  const fi::gemm::Plan pl = fi::gemm::plan(M, N, K);
+  const size_t split = split_bytes(M, N, pl);
+  return fuse_norm(M, K, pl) ? split : norm_rows_bytes(M, K) + split;
+}
+
+extern "C" int fi_rmsnorm_int4_matmul(const void* x, int64_t x_stride, int64_t M, int64_t K,
+                                      const void* norm_weight, float eps, const void* w,
+                                      int64_t w_stride, const void* scales, int64_t s_stride,
+                                      int64_t N, int64_t groupsize, void* out,
+                                      int64_t out_stride, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+  using namespace fi;
+  using namespace fi::gemm;
+  clear_error();
+  int rc = check_linear("fi_rmsnorm_int4_matmul", x, x_stride, M, K, w, w_stride, scales,
+                        s_stride, N, groupsize, out, out_stride);
+  if (rc != FI_OK || M == 0 || N == 0) return rc;
+  if (!norm_weight || ((uintptr_t)norm_weight & 15)) {
+    set_error("fi_rmsnorm_int4_matmul: norm weight missing or not 16-byte aligned");
+    return FI_ERR_INVALID;
+  }
+  const Plan pl = plan(M, N, K);
+  const bool fused = fuse_norm(M, K, pl);
+  const size_t rows = fused ? 0 : norm_rows_bytes(M, K);
+  const size_t need = rows + split_bytes(M, N, pl);
+  if (need && (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255))) {
+    set_error("fi_rmsnorm_int4_matmul: workspace of %zu bytes needed (have %zu)", need,
+              workspace ? workspace_bytes : (size_t)0);
+    return FI_ERR_WORKSPACE;
+  }
+  if ((M + pl.mt - 1) / pl.mt > 65535) {
+    set_error("fi_rmsnorm_int4_matmul: M %lld too large", (long long)M);
+    return FI_ERR_UNSUPPORTED;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  Params p = make_params(x, x_stride, M, K, w, w_stride, scales, s_stride, N, out, out_stride);
+  p.norm_w = (const half_t*)norm_weight;
+  p.eps = eps;
+  if (fused) {
+    launch_linear<true>(p, scales != nullptr, pl, workspace, st);
+  } else {
+    half_t* normed = (half_t*)workspace;
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, st,
+                       (const half_t*)x, x_stride, (int)M, (int)K, (const half_t*)norm_weight,
+                       eps, normed, K);
+    p.x = normed;
+    p.x_stride = K;
+    launch_linear<false>(p, scales != nullptr, pl, (char*)workspace + rows, st);
+  }
+  return check_launch("fi_rmsnorm_int4_matmul");
+}
+
+extern "C" int fi_rmsnorm(const void* x, int64_t x_stride, int64_t M, int64_t hidden,
+                          const void* weight, float eps, void* out, int64_t out_stride,
+                          void* stream) {
+  using namespace fi;
+  using namespace fi::gemm;
+  clear_error();
+  if (M < 0 || hidden < 0 || hidden >= (1ll << 30) || M >= (1ll << 30)) {
+    set_error("fi_rmsnorm: invalid sizes M %lld hidden %lld", (long long)M, (long long)hidden);
+    return FI_ERR_INVALID;
+  }
+  if (M == 0 || hidden == 0) return FI_OK;
+  if (hidden % 8) {
+    set_error("fi_rmsnorm: hidden %lld must be a multiple of 8", (long long)hidden);
+    return FI_ERR_UNSUPPORTED;
+  }
+  if (!x || !weight || !out) {
+    set_error("fi_rmsnorm: null pointer");
+    return FI_ERR_INVALID;
+  }
+  if (((uintptr_t)x & 15) || ((uintptr_t)weight & 15) || ((uintptr_t)out & 15) ||
+      x_stride % 8 || out_stride % 8 || x_stride < hidden || out_stride < hidden) {
+    set_error("fi_rmsnorm: rows must be 16-byte aligned and strides cover the rows");
+    return FI_ERR_INVALID;
+  }
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0,
+                     (hipStream_t)stream, (const half_t*)x, x_stride, (int)M, (int)hidden,
+                     (const half_t*)weight, eps, (half_t*)out, out_stride);
+  return check_launch("fi_rmsnorm");
 }
 
 extern "C" int fi_int4_quantize(const void* w, int64_t w_stride, int64_t N, int64_t K,

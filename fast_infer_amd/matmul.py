@@ -5,7 +5,8 @@
 dequantization then runs inside the MFMA loop — or an fp16 ``[N, K]`` weight.
 ``quantize_int4_groupwise`` (loader.py:9-41) and ``dequantize_int4`` (the reference's
 ``_dequant_storage``, matmul.py:197-214) produce and expand the same wire format, bit for
-bit.
+bit.  ``rms_norm`` is kernels/rms_norm.py's; ``rms_norm_int4_matmul`` is the norm of
+model.py:82 and the projection after it in one call.
 """
 
 from __future__ import annotations
@@ -53,27 +54,7 @@ def int4_matmul(x: torch.Tensor, w, scales=None, groupsize: int = 128, *,
     (optional) must not be shared by calls that overlap in time; by default one cached
     workspace per device and stream is used."""
     _need_cuda("x", x)
-    if isinstance(w, tuple):
-        packed, sc = w
-        _need_cuda("packed", packed)
-        if packed.dtype not in (torch.int8, torch.uint8) or packed.dim() != 2:
-            raise TypeError("packed weights must be a 2-D int8 tensor")
-        if sc.dtype != torch.float16 or sc.dim() != 2:
-            raise TypeError("scales must be a 2-D float16 tensor")
-        N, K = packed.shape[0], packed.shape[1] * 2
-        if sc.shape[0] != N or sc.shape[1] * groupsize != K:
-            raise ValueError(f"scales {tuple(sc.shape)} do not match packed {tuple(packed.shape)}")
-        wt = _rows16(packed, 1)
-        if sc.stride(-1) != 1:
-            sc = sc.contiguous()
-        w_stride, s_ptr, s_stride = wt.stride(0), sc.data_ptr(), sc.stride(0)
-    else:
-        _need_cuda("w", w)
-        if w.dtype != torch.float16 or w.dim() != 2:
-            raise TypeError("w must be a 2-D float16 tensor or a (packed, scales) tuple")
-        N, K = w.shape
-        wt = _rows16(w, 2)
-        w_stride, s_ptr, s_stride = wt.stride(0), None, 0
+    N, K, wt, w_stride, s_ptr, s_stride, _keep = _weight_args(w, groupsize)
     if x.shape[-1] != K:
         raise ValueError(f"x has K = {x.shape[-1]}, the weight K = {K}")
     if K % groupsize:
@@ -97,6 +78,86 @@ def int4_matmul(x: torch.Tensor, w, scales=None, groupsize: int = 128, *,
                             s_stride, N, groupsize, out.data_ptr(), out.stride(0), ws_ptr,
                             ws_bytes, stream)
     _lib.check(rc, "int4_matmul")
+    return out.reshape(*lead, N)
+
+
+def _weight_args(w, groupsize: int):
+    """(N, K, weight tensor, its row stride, scales pointer, scales row stride, scales
+    tensor kept alive for the call) for either weight form."""
+    if isinstance(w, tuple):
+        packed, sc = w
+        _need_cuda("packed", packed)
+        if packed.dtype not in (torch.int8, torch.uint8) or packed.dim() != 2:
+            raise TypeError("packed weights must be a 2-D int8 tensor")
+        if sc.dtype != torch.float16 or sc.dim() != 2:
+            raise TypeError("scales must be a 2-D float16 tensor")
+        N, K = packed.shape[0], packed.shape[1] * 2
+        if sc.shape[0] != N or sc.shape[1] * groupsize != K:
+            raise ValueError(f"scales {tuple(sc.shape)} do not match packed {tuple(packed.shape)}")
+        wt = _rows16(packed, 1)
+        if sc.stride(-1) != 1:
+            sc = sc.contiguous()
+        return N, K, wt, wt.stride(0), sc.data_ptr(), sc.stride(0), sc
+    _need_cuda("w", w)
+    if w.dtype != torch.float16 or w.dim() != 2:
+        raise TypeError("w must be a 2-D float16 tensor or a (packed, scales) tuple")
+    N, K = w.shape
+    wt = _rows16(w, 2)
+    return N, K, wt, wt.stride(0), None, 0, None
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5) -> torch.Tensor:
+    """kernels/rms_norm.py:29-43: ``x * rsqrt(mean(x^2) + eps) * weight`` in fp32, fp16
+    out, over the last dimension of ``x [..., hidden]``."""
+    _need_cuda("x", x)
+    hidden = x.shape[-1]
+    if weight.shape != (hidden,):
+        raise ValueError(f"weight {tuple(weight.shape)} does not match hidden {hidden}")
+    if x.dtype != torch.float16:
+        x = x.to(torch.float16)
+    wt = weight.to(device=x.device, dtype=torch.float16).contiguous()
+    x2 = _rows16(x.reshape(-1, hidden), 2)
+    out = torch.empty(x2.shape, dtype=torch.float16, device=x.device)
+    if x2.shape[0]:
+        rc = _lib.load().fi_rmsnorm(x2.data_ptr(), x2.stride(0), x2.shape[0], hidden,
+                                    wt.data_ptr(), float(eps), out.data_ptr(), out.stride(0),
+                                    _lib.stream_handle(x.device))
+        _lib.check(rc, "rms_norm")
+    return out.reshape(x.shape)
+
+
+def rms_norm_int4_matmul(x: torch.Tensor, norm_weight: torch.Tensor, w, eps: float = 1e-5,
+                         groupsize: int = 128, *,
+                         workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """``int4_matmul(rms_norm(x, norm_weight, eps), w)`` in one call (model.py:82 and the
+    QKV projection after it): for few rows the norm is applied inside the GEMM."""
+    _need_cuda("x", x)
+    N, K, wt, w_stride, s_ptr, s_stride, _keep = _weight_args(w, groupsize)
+    if x.shape[-1] != K or norm_weight.shape != (K,):
+        raise ValueError(f"x {tuple(x.shape)} / norm weight {tuple(norm_weight.shape)} do not "
+                         f"match K = {K}")
+    if K % groupsize:
+        raise ValueError(f"K ({K}) must be multiple of groupsize ({groupsize})")
+    if x.dtype != torch.float16:
+        x = x.to(torch.float16)
+    nw = norm_weight.to(device=x.device, dtype=torch.float16).contiguous()
+    lead = x.shape[:-1]
+    x2 = _rows16(x.reshape(-1, K), 2)
+    M = x2.shape[0]
+    out = torch.empty(M, N, dtype=torch.float16, device=x.device)
+    if M == 0 or N == 0:
+        return out.reshape(*lead, N)
+    lib = _lib.load()
+    stream = _lib.stream_handle(x.device)
+    need = lib.fi_rmsnorm_int4_matmul_workspace_size(M, N, K)
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = _workspace(x.device, stream, need)
+    ws_ptr = workspace.data_ptr() if need else None
+    ws_bytes = workspace.numel() * workspace.element_size() if need else 0
+    rc = lib.fi_rmsnorm_int4_matmul(x2.data_ptr(), x2.stride(0), M, K, nw.data_ptr(), float(eps),
+                                    wt.data_ptr(), w_stride, s_ptr, s_stride, N, groupsize,
+                                    out.data_ptr(), out.stride(0), ws_ptr, ws_bytes, stream)
+    _lib.check(rc, "rms_norm_int4_matmul")
     return out.reshape(*lead, N)
 
 

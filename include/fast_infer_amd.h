@@ -273,6 +273,31 @@ FI_API int fi_int4_matmul(const void* x, int64_t x_stride, int64_t M, int64_t K,
                    void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * RMSNorm (kernels/rms_norm.py:29-43, rms_norm): out[m] = fp16((x[m] * r) * weight) with
+ * r = rsqrt(sum(x[m]^2) / hidden + eps), all in fp32 (rms_norm.py:17-24).
+ *   x, out: fp16 [M, hidden] (row strides in elements, 16-byte aligned rows);
+ *   weight: fp16 [hidden]; hidden a multiple of 8.
+ */
+FI_API int fi_rmsnorm(const void* x, int64_t x_stride, int64_t M, int64_t hidden,
+               const void* weight, float eps, void* out, int64_t out_stride, void* stream);
+
+/*
+ * rms_norm followed by int4_matmul as one call (model.py:82 then :87 / :91-93): out =
+ * fi_int4_matmul(fi_rmsnorm(x, norm_weight, eps), w, scales).  Up to a few rows the norm is
+ * applied inside the GEMM's X operand (each workgroup computes its rows' r), saving the
+ * separate pass and its write and read of the normalized rows; above that a separate norm
+ * pass writes them into the workspace first.  Arguments as fi_rmsnorm and
+ * fi_int4_matmul; workspace: fi_rmsnorm_int4_matmul_workspace_size(M, N, K) bytes,
+ * 256-byte aligned, when non-zero.
+ */
+FI_API size_t fi_rmsnorm_int4_matmul_workspace_size(int64_t M, int64_t N, int64_t K);
+FI_API int fi_rmsnorm_int4_matmul(const void* x, int64_t x_stride, int64_t M, int64_t K,
+                           const void* norm_weight, float eps, const void* w,
+                           int64_t w_stride, const void* scales, int64_t s_stride,
+                           int64_t N, int64_t groupsize, void* out, int64_t out_stride,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * quantize_int4_groupwise (loader.py:9-41) on the device, bit-exact with the reference's
  * fp16 tensor arithmetic on a CUDA device: amax = max |w| over each 128-wide group,
  * clamped below at fp16(1e-6); scale = fp16(fp32(amax) * fp32(1/7)); q =

@@ -35,7 +35,8 @@ def test_header_declares_entry_points():
     for n in ("fi_flash_attention_fwd", "fi_paged_attention_fwd", "fi_kv_store",
               "fi_rope_store_kv", "fi_kv_append", "fi_kv_release", "fi_kv_reset",
               "fi_int4_matmul", "fi_int4_matmul_workspace_size", "fi_int4_quantize",
-              "fi_int4_dequantize",
+              "fi_int4_dequantize", "fi_rmsnorm", "fi_rmsnorm_int4_matmul",
+              "fi_rmsnorm_int4_matmul_workspace_size",
               "fi_paged_attention_workspace_size", "fi_last_error", "fi_version"):
         assert n in names
 
@@ -181,6 +182,25 @@ def test_int4_validation(lib):
     assert lib.fi_int4_matmul(16, 256, 0, 256, 16, 128, 16, 2, 64, 128, 16, 64, None, 0,
                               None) == _lib.FI_OK
     assert lib.fi_int4_quantize(16, 256, 0, 256, 128, 16, 128, 16, 2, None) == _lib.FI_OK
+
+
+def test_rmsnorm_validation(lib):
+    from fast_infer_amd import _lib
+
+    assert lib.fi_rmsnorm(16, 100, 2, 100, 16, 1e-5, 16, 100, None) == _lib.FI_ERR_UNSUPPORTED
+    assert lib.fi_rmsnorm(18, 256, 2, 256, 16, 1e-5, 16, 256, None) == _lib.FI_ERR_INVALID
+    assert lib.fi_rmsnorm(None, 256, 2, 256, 16, 1e-5, 16, 256, None) == _lib.FI_ERR_INVALID
+    assert lib.fi_rmsnorm(16, 256, 0, 256, 16, 1e-5, 16, 256, None) == _lib.FI_OK
+    # fused: norm weight missing, misaligned, or the separate-pass workspace missing
+    assert lib.fi_rmsnorm_int4_matmul(16, 3072, 1, 3072, None, 1e-5, 16, 1536, 16, 24, 5120,
+                                      128, 16, 5120, None, 0, None) == _lib.FI_ERR_INVALID
+    assert lib.fi_rmsnorm_int4_matmul(16, 3072, 1, 3072, 24, 1e-5, 16, 1536, 16, 24, 5120,
+                                      128, 16, 5120, None, 0, None) == _lib.FI_ERR_INVALID
+    assert lib.fi_rmsnorm_int4_matmul_workspace_size(1, 5120, 3072) == 0
+    need = lib.fi_rmsnorm_int4_matmul_workspace_size(64, 5120, 3072)
+    assert need >= 64 * 3072 * 2
+    assert lib.fi_rmsnorm_int4_matmul(16, 3072, 64, 3072, 16, 1e-5, 16, 1536, 16, 24, 5120,
+                                      128, 16, 5120, None, 0, None) == _lib.FI_ERR_WORKSPACE
 
 
 def test_workspace_size(lib):
