@@ -41,6 +41,10 @@ FILE_FLAGS = {
 }
 
 
+# rocBLAS runs the plain fp16 GEMM of prefill-sized linear layers (int4_gemm.hip).
+LINK_LIBS = ["-lrocblas"]
+
+
 def _hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and Path(cand).exists():
@@ -68,7 +72,8 @@ def build_library(verbose: bool = False, extra_flags: list[str] | None = None) -
     with cf.ThreadPoolExecutor(max_workers=min(8, len(sources))) as ex:
         objs = list(ex.map(lambda s: _compile(hipcc, s, extra), sources))
     tmp = LIB_PATH.with_suffix(".so.tmp")
-    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), *LINK_LIBS,
+           "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{res.stdout}{res.stderr}")

@@ -16,9 +16,11 @@
 // operand.  In k-step s (0..3) of a group, lane group g = lane/16 supplies k = 32g + 8s
 // .. +7: the 16 bytes one lane loads are exactly its four k-steps.  Small grids split the
 // K groups over blockIdx.z; a second kernel adds the fp32 partials in a fixed order.
+#include <rocblas/rocblas.h>
 #include <stdlib.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "common.h"
 
@@ -307,6 +309,55 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(Params p) {
   store_tile<kMSub>(p, acc, m0, blockIdx.x * kNTile);
 }
 
+// Prefill-sized calls: the MFMA kernels above spend most of their time dequantizing (each
+// weight is dequantized once per row tile) at these sizes, so the weight is dequantized once
+// into the workspace and the plain fp16 GEMM runs in rocBLAS (fp16 in and out, fp32
+// accumulation).  One rocBLAS handle per device, created on first use; the stream is set
+// per call under a lock.
+struct BlasState {
+  std::mutex mu;
+  rocblas_handle handle[64] = {};
+};
+
+inline BlasState& blas_state() {
+  static BlasState s;
+  return s;
+}
+
+// C[M, N] (ldc) = X[M, K] (ldx) * W[N, K]^T (ldw), all fp16 row-major, fp32 accumulation.
+inline int blas_gemm(const half_t* x, int64_t ldx, const half_t* w, int64_t ldw, half_t* out,
+                     int64_t ldc, int M, int N, int K, hipStream_t st) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    set_error("fi_int4_matmul: no current HIP device");
+    return FI_ERR_HIP;
+  }
+  BlasState& bs = blas_state();
+  std::lock_guard<std::mutex> lock(bs.mu);
+  if (!bs.handle[dev] && rocblas_create_handle(&bs.handle[dev]) != rocblas_status_success) {
+    bs.handle[dev] = nullptr;
+    set_error("fi_int4_matmul: rocblas_create_handle failed");
+    return FI_ERR_HIP;
+  }
+  rocblas_handle h = bs.handle[dev];
+  if (rocblas_set_stream(h, st) != rocblas_status_success) {
+    set_error("fi_int4_matmul: rocblas_set_stream failed");
+    return FI_ERR_HIP;
+  }
+  const float alpha = 1.f, beta = 0.f;
+  // column-major view: C^T [N, M] = op(W^T)^T ... = W [N, K] x X^T [K, M]
+  const rocblas_status rs = rocblas_gemm_ex(
+      h, rocblas_operation_transpose, rocblas_operation_none, N, M, K, &alpha, w,
+      rocblas_datatype_f16_r, (rocblas_int)ldw, x, rocblas_datatype_f16_r, (rocblas_int)ldx, &beta,
+      out, rocblas_datatype_f16_r, (rocblas_int)ldc, out, rocblas_datatype_f16_r,
+      (rocblas_int)ldc, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+  if (rs != rocblas_status_success) {
+    set_error("fi_int4_matmul: rocblas_gemm_ex failed (%d)", (int)rs);
+    return FI_ERR_HIP;
+  }
+  return FI_OK;
+}
+
 // Decode-sized calls (16 rows of X per blockIdx.y): one workgroup per 16 output columns.
 // The four waves take interleaved groups (g = wave, wave + 4, ...), so K is split inside
 // the workgroup and no partials leave it.  Each lane issues the loads of kChunk groups at
@@ -484,6 +535,7 @@ struct Plan {
   int mt;
   int splits;
   int gemv_rows;
+  bool library;  // prefill-sized: dequantize once, then a plain fp16 GEMM (rocBLAS)
 };
 
 inline int gemv_limit() {
@@ -502,6 +554,14 @@ inline int env_int(const char* name, int dflt) {
 inline Plan plan(int64_t M, int64_t N, int64_t K) {
   Plan pl;
   pl.gemv_rows = 0;
+  pl.library = false;
+  static const int lib_min_m = env_int("FI_INT4_LIBRARY_MIN_M", 129);
+  if (lib_min_m > 0 && M >= lib_min_m) {
+    pl.library = true;
+    pl.mt = 0;
+    pl.splits = 1;
+    return pl;
+  }
   if (M <= gemv_limit() && (M + 15) / 16 <= 65535) {
     pl.gemv_rows = 16;
     pl.mt = 16;
@@ -530,15 +590,12 @@ inline Plan plan(int64_t M, int64_t N, int64_t K) {
 }  // namespace gemm
 }  // namespace fi
 
-extern "C" size_t fi_int4_matmul_workspace_size(int64_t M, int64_t N, int64_t K) {
-  if (M <= 0 || N <= 0 || K <= 0 || K % fi::gemm::kGroup) return 0;
-  const fi::gemm::Plan pl = fi::gemm::plan(M, N, K);
-  return pl.splits > 1 ? (size_t)pl.splits * M * N * sizeof(float) : 0;
-}
-
 namespace {
 
 using fi::half_t;
+using fi::gemm::blas_gemm;
+using fi::gemm::dequantize_kernel;
+using fi::gemm::rmsnorm_kernel;
 
 // Shared validation for the linear-layer entry points; FI_OK when the operands are usable.
 int check_linear(const char* fn, const void* x, int64_t x_stride, int64_t M, int64_t K,
@@ -660,9 +717,89 @@ bool fuse_norm(int64_t M, int64_t K, const fi::gemm::Plan& pl) {
   return pl.gemv_rows && M <= max_m && std::min<int64_t>(M, 16) * K * 2 <= 65536;
 }
 
-size_t norm_rows_bytes(int64_t M, int64_t K) { return (size_t)((M * K * 2 + 255) / 256 * 256); }
+size_t round256(int64_t n) { return (size_t)((n + 255) / 256 * 256); }
+
+size_t norm_rows_bytes(int64_t M, int64_t K) { return round256(M * K * 2); }
+
+// Workspace layout of a call: [normalized rows (separate norm pass)] [dequantized weight
+// (library path, packed weights)] [fp32 partials (split K)], each 256-byte aligned.
+struct Layout {
+  size_t rows, weight, split, total;
+};
+
+Layout layout(int64_t M, int64_t N, int64_t K, const fi::gemm::Plan& pl, bool int4, bool norm) {
+  Layout l;
+  l.rows = norm && !fuse_norm(M, K, pl) ? norm_rows_bytes(M, K) : 0;
+  l.weight = pl.library && int4 ? round256(N * K * 2) : 0;
+  l.split = round256((int64_t)split_bytes(M, N, pl));
+  l.total = l.rows + l.weight + l.split;
+  return l;
+}
+
+// One linear-layer call on any path; norm_w non-null applies RMSNorm to X first.
+int run_linear(const char* fn, const void* x, int64_t x_stride, int64_t M, int64_t K,
+               const void* norm_w, float eps, const void* w, int64_t w_stride,
+               const void* scales, int64_t s_stride, int64_t N, void* out, int64_t out_stride,
+               void* workspace, size_t workspace_bytes, hipStream_t st) {
+  using namespace fi;
+  using namespace fi::gemm;
+  const bool int4 = scales != nullptr;
+  const bool norm = norm_w != nullptr;
+  const Plan pl = plan(M, N, K);
+  const Layout l = layout(M, N, K, pl, int4, norm);
+  if (l.total && (!workspace || workspace_bytes < l.total || ((uintptr_t)workspace & 255))) {
+    set_error("%s: workspace of %zu bytes (256-byte aligned) needed, %zu given", fn, l.total,
+              workspace ? workspace_bytes : (size_t)0);
+    return FI_ERR_WORKSPACE;
+  }
+  if (!pl.library && (M + (pl.mt ? pl.mt : 16) - 1) / (pl.mt ? pl.mt : 16) > 65535) {
+    set_error("%s: M %lld too large", fn, (long long)M);
+    return FI_ERR_UNSUPPORTED;
+  }
+  char* ws = (char*)workspace;
+  Params p = make_params(x, x_stride, M, K, w, w_stride, scales, s_stride, N, out, out_stride);
+  if (norm && fuse_norm(M, K, pl)) {
+    p.norm_w = (const half_t*)norm_w;
+    p.eps = eps;
+    launch_linear<true>(p, int4, pl, nullptr, st);
+    return check_launch(fn);
+  }
+  if (norm) {  // separate norm pass into the workspace
+    half_t* normed = (half_t*)ws;
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, st,
+                       (const half_t*)x, x_stride, (int)M, (int)K, (const half_t*)norm_w, eps,
+                       normed, K);
+    p.x = normed;
+    p.x_stride = K;
+  }
+  if (pl.library) {
+    const half_t* w16 = (const half_t*)w;
+    int64_t ldw = w_stride;
+    if (int4) {  // dequantize once into the workspace
+      half_t* deq = (half_t*)(ws + l.rows);
+      const int64_t items = N * (K / 8);
+      const int64_t blocks = std::min<int64_t>((items + 255) / 256, 65536);
+      hipLaunchKernelGGL(dequantize_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
+                         (const uint8_t*)w, w_stride, (const half_t*)scales, s_stride, (int)N,
+                         (int)K, deq, K);
+      w16 = deq;
+      ldw = K;
+    }
+    const int rc = check_launch(fn);
+    if (rc != FI_OK) return rc;
+    return blas_gemm(p.x, p.x_stride, w16, ldw, (half_t*)out, out_stride, (int)M, (int)N,
+                     (int)K, st);
+  }
+  launch_linear<false>(p, int4, pl, ws + l.rows + l.weight, st);
+  return check_launch(fn);
+}
 
 }  // namespace
+
+extern "C" size_t fi_int4_matmul_workspace_size(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % fi::gemm::kGroup) return 0;
+  return layout(M, N, K, fi::gemm::plan(M, N, K), true, false).total;  // the larger form
+}
 
 extern "C" int fi_int4_matmul(const void* x, int64_t x_stride, int64_t M, int64_t K,
                               const void* w, int64_t w_stride, const void* scales,
@@ -670,33 +807,17 @@ extern "C" int fi_int4_matmul(const void* x, int64_t x_stride, int64_t M, int64_
                               int64_t out_stride, void* workspace, size_t workspace_bytes,
                               void* stream) {
   using namespace fi;
-  using namespace fi::gemm;
   clear_error();
   int rc = check_linear("fi_int4_matmul", x, x_stride, M, K, w, w_stride, scales, s_stride, N,
                         groupsize, out, out_stride);
   if (rc != FI_OK || M == 0 || N == 0) return rc;
-  const Plan pl = plan(M, N, K);
-  const size_t need = split_bytes(M, N, pl);
-  if (need && (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 15))) {
-    set_error("fi_int4_matmul: workspace of %zu bytes needed (have %zu)", need,
-              workspace ? workspace_bytes : (size_t)0);
-    return FI_ERR_WORKSPACE;
-  }
-  if ((M + pl.mt - 1) / pl.mt > 65535) {
-    set_error("fi_int4_matmul: M %lld too large", (long long)M);
-    return FI_ERR_UNSUPPORTED;
-  }
-  launch_linear<false>(make_params(x, x_stride, M, K, w, w_stride, scales, s_stride, N, out,
-                                   out_stride),
-                       scales != nullptr, pl, workspace, (hipStream_t)stream);
-  return check_launch("fi_int4_matmul");
+  return run_linear("fi_int4_matmul", x, x_stride, M, K, nullptr, 0.f, w, w_stride, scales,
+                    s_stride, N, out, out_stride, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 extern "C" size_t fi_rmsnorm_int4_matmul_workspace_size(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0 || K % fi::gemm::kGroup) return 0;
-  const fi::gemm::Plan pl = fi::gemm::plan(M, N, K);
-  const size_t split = split_bytes(M, N, pl);
-  return fuse_norm(M, K, pl) ? split : norm_rows_bytes(M, K) + split;
+  return layout(M, N, K, fi::gemm::plan(M, N, K), true, true).total;
 }
 
 extern "C" int fi_rmsnorm_int4_matmul(const void* x, int64_t x_stride, int64_t M, int64_t K,
@@ -706,7 +827,6 @@ extern "C" int fi_rmsnorm_int4_matmul(const void* x, int64_t x_stride, int64_t M
                                       int64_t out_stride, void* workspace,
                                       size_t workspace_bytes, void* stream) {
   using namespace fi;
-  using namespace fi::gemm;
   clear_error();
   int rc = check_linear("fi_rmsnorm_int4_matmul", x, x_stride, M, K, w, w_stride, scales,
                         s_stride, N, groupsize, out, out_stride);
@@ -715,35 +835,9 @@ extern "C" int fi_rmsnorm_int4_matmul(const void* x, int64_t x_stride, int64_t M
     set_error("fi_rmsnorm_int4_matmul: norm weight missing or not 16-byte aligned");
     return FI_ERR_INVALID;
   }
-  const Plan pl = plan(M, N, K);
-  const bool fused = fuse_norm(M, K, pl);
-  const size_t rows = fused ? 0 : norm_rows_bytes(M, K);
-  const size_t need = rows + split_bytes(M, N, pl);
-  if (need && (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255))) {
-    set_error("fi_rmsnorm_int4_matmul: workspace of %zu bytes needed (have %zu)", need,
-              workspace ? workspace_bytes : (size_t)0);
-    return FI_ERR_WORKSPACE;
-  }
-  if ((M + pl.mt - 1) / pl.mt > 65535) {
-    set_error("fi_rmsnorm_int4_matmul: M %lld too large", (long long)M);
-    return FI_ERR_UNSUPPORTED;
-  }
-  hipStream_t st = (hipStream_t)stream;
-  Params p = make_params(x, x_stride, M, K, w, w_stride, scales, s_stride, N, out, out_stride);
-  p.norm_w = (const half_t*)norm_weight;
-  p.eps = eps;
-  if (fused) {
-    launch_linear<true>(p, scales != nullptr, pl, workspace, st);
-  } else {
-    half_t* normed = (half_t*)workspace;
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, st,
-                       (const half_t*)x, x_stride, (int)M, (int)K, (const half_t*)norm_weight,
-                       eps, normed, K);
-    p.x = normed;
-    p.x_stride = K;
-    launch_linear<false>(p, scales != nullptr, pl, (char*)workspace + rows, st);
-  }
-  return check_launch("fi_rmsnorm_int4_matmul");
+  return run_linear("fi_rmsnorm_int4_matmul", x, x_stride, M, K, norm_weight, eps, w, w_stride,
+                    scales, s_stride, N, out, out_stride, workspace, workspace_bytes,
+                    (hipStream_t)stream);
 }
 
 extern "C" int fi_rmsnorm(const void* x, int64_t x_stride, int64_t M, int64_t hidden,

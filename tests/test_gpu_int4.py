@@ -6,7 +6,7 @@
 * int4_matmul with packed weights within the fp32-accumulation bound of the float64
   product on the dequantized weights, for decode-sized M (1..64, split-K) and prefill
   sizes, odd N, strided X; the speed mode (dequantized fp16 weights) within the same
-  bound, and equal bit for bit where both run the same tiled kernel (prefill sizes).
+  bound.
 """
 
 import numpy as np
@@ -92,8 +92,8 @@ def test_int4_matmul_strided_x_and_batch_dims(hip):
 
 
 def test_int4_matmul_prefill_size_sampled(hip):
-    """4 x 512 tokens through the fused QKV weight (N 5120, K 3072): sampled rows against
-    float64, every row equal to the speed-mode result."""
+    """4 x 512 tokens through the fused QKV weight (N 5120, K 3072): sampled rows of the
+    packed and the dequantized forms against float64."""
     banner("int4_matmul M=2048 N=5120 K=3072")
     from fast_infer_amd import dequantize_int4, int4_matmul, quantize_int4_groupwise
 
@@ -104,9 +104,10 @@ def test_int4_matmul_prefill_size_sampled(hip):
     x = torch.randn(M, K, device=DEV, generator=g).half()
     out = int4_matmul(x, (packed, scales))
     w16 = dequantize_int4(packed, scales)
-    assert torch.equal(out, int4_matmul(x, w16))   # same tiled kernel: same bits
-    rows = torch.tensor([0, 1, 127, 128, 1000, 2047])
+    out16 = int4_matmul(x, w16)
+    rows = torch.tensor([0, 1, 63, 64, 127, 128, 1000, 2047])
     _check(out[rows.to(DEV)], x[rows.to(DEV)].cpu().numpy(), w16.cpu().numpy())
+    _check(out16[rows.to(DEV)], x[rows.to(DEV)].cpu().numpy(), w16.cpu().numpy())
 
 
 def test_int4_matmul_workspace(hip):
@@ -120,7 +121,9 @@ def test_int4_matmul_workspace(hip):
     N, K = 5120, 3072
     M = 40
     need = lib.fi_int4_matmul_workspace_size(M, N, K)
-    assert need > 0 and lib.fi_int4_matmul_workspace_size(4096, N, K) == 0
+    assert need > 0
+    # prefill sizes dequantize the packed weight once into the workspace
+    assert lib.fi_int4_matmul_workspace_size(4096, N, K) == N * K * 2
     w = _weights(12, N, K, 0.02)
     packed, scales = quantize_int4_groupwise(torch.from_numpy(w).to(DEV))
     w16 = dequantize_int4(packed, scales)
@@ -134,5 +137,26 @@ def test_int4_matmul_workspace(hip):
     out = torch.empty(M, N, dtype=torch.float16, device=DEV)
     rc = lib.fi_int4_matmul(x.data_ptr(), K, M, K, w16.data_ptr(), K, None, 0, N, 128,
                             out.data_ptr(), N, ws.data_ptr(), need - 16,
+                            _lib.stream_handle(torch.device(DEV)))
+    assert rc == _lib.FI_ERR_WORKSPACE
+
+
+def test_int4_matmul_prefill_workspace_and_errors(hip):
+    """The prefill path (dequantize once + fp16 GEMM): a caller workspace gives the same
+    bits as the cached one, and one too small is rejected before launch."""
+    banner("int4_matmul prefill workspace")
+    from fast_infer_amd import _lib, int4_matmul, quantize_int4_groupwise
+
+    lib = _lib.load()
+    M, N, K = 512, 640, 1024
+    w = _weights(13, N, K, 0.02)
+    packed, scales = quantize_int4_groupwise(torch.from_numpy(w).to(DEV))
+    x = torch.randn(M, K, device=DEV).half()
+    need = lib.fi_int4_matmul_workspace_size(M, N, K)
+    ws = torch.empty(need, dtype=torch.uint8, device=DEV)
+    assert torch.equal(int4_matmul(x, (packed, scales), workspace=ws), int4_matmul(x, (packed, scales)))
+    out = torch.empty(M, N, dtype=torch.float16, device=DEV)
+    rc = lib.fi_int4_matmul(x.data_ptr(), K, M, K, packed.data_ptr(), K // 2, scales.data_ptr(),
+                            K // 128, N, 128, out.data_ptr(), N, ws.data_ptr(), need - 256,
                             _lib.stream_handle(torch.device(DEV)))
     assert rc == _lib.FI_ERR_WORKSPACE
