@@ -253,6 +253,23 @@ def test_paged_decode_strided_q(hip):
     assert _maxabs(out, OA.paged_attention(q, kc, vc, table, sp["bs"], lens)) <= ATOL
 
 
+@pytest.mark.parametrize("Hq,Hkv", [(15, 5), (64, 2), (12, 6), (6, 1), (40, 8)])
+def test_paged_decode_head_layouts(hip, Hq, Hkv):
+    # Odd kv-head counts and groups wider than one workgroup (64/2: 32 query heads per kv
+    # head, served by two workgroups) take the one-kv-head-per-wave launch; even counts
+    # with whole groups take the two-heads-per-wave launch.  Both against the oracle.
+    banner(f"paged decode heads {Hq}/{Hkv}")
+    from fast_infer_amd import paged_attention
+
+    sp = dict(B=3, Hq=Hq, Hkv=Hkv, D=128, bs=64, N=24, lens=[1, 190, 70], seed=40 + Hq)
+    q, kc, vc, table, lens = specs.decode_inputs(sp)
+    cl = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    out = paged_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), table.to(DEV), 64, max(lens),
+                          context_lens=cl)
+    torch.cuda.synchronize()
+    assert _maxabs(out, OA.paged_attention(q, kc, vc, table, 64, lens)) <= ATOL
+
+
 def _big_decode_inputs(B, lens, N, seed):
     g = torch.Generator(device=DEV).manual_seed(seed)
     q = torch.randn(B, 24, 128, device=DEV, generator=g).half()
