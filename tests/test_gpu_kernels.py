@@ -253,15 +253,19 @@ def test_paged_decode_strided_q(hip):
     assert _maxabs(out, OA.paged_attention(q, kc, vc, table, sp["bs"], lens)) <= ATOL
 
 
-@pytest.mark.parametrize("Hq,Hkv", [(15, 5), (64, 2), (12, 6), (6, 1), (40, 8)])
-def test_paged_decode_head_layouts(hip, Hq, Hkv):
-    # Odd kv-head counts and groups wider than one workgroup (64/2: 32 query heads per kv
-    # head, served by two workgroups) take the one-kv-head-per-wave launch; even counts
-    # with whole groups take the two-heads-per-wave launch.  Both against the oracle.
-    banner(f"paged decode heads {Hq}/{Hkv}")
+@pytest.mark.parametrize("Hq,Hkv", [(15, 5), (64, 2), (12, 6), (6, 1), (40, 8), (24, 8),
+                                     (16, 8), (32, 4), (8, 8)])
+@pytest.mark.parametrize("batch", [3, 9])
+def test_paged_decode_head_layouts(hip, Hq, Hkv, batch):
+    # GQA groups of 1..8 query heads per kv head, odd kv-head counts (15/5, 6/1) and a
+    # group wider than one workgroup's 16 MFMA columns (64/2: 32 query heads per kv head,
+    # served by two workgroups), at 3 rows (one partition) and 9 rows with contexts past
+    # 512 (split partitions and the merge).  Every layout against the oracle.
+    banner(f"paged decode heads {Hq}/{Hkv} batch {batch}")
     from fast_infer_amd import paged_attention
 
-    sp = dict(B=3, Hq=Hq, Hkv=Hkv, D=128, bs=64, N=24, lens=[1, 190, 70], seed=40 + Hq)
+    lens = [1, 190, 70, 600, 513, 64, 65, 300, 1000][:batch]
+    sp = dict(B=batch, Hq=Hq, Hkv=Hkv, D=128, bs=64, N=64, lens=lens, seed=40 + Hq)
     q, kc, vc, table, lens = specs.decode_inputs(sp)
     cl = torch.tensor(lens, dtype=torch.int32, device=DEV)
     out = paged_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), table.to(DEV), 64, max(lens),
