@@ -165,6 +165,40 @@ __device__ __forceinline__ void write_pool(const Params& p, const char* stage, i
   }
 }
 
+// The same copy split by wave: wave w stores exactly the LDS bytes its own copy
+// instructions of a later tile overwrite (K keys 16w..16w+15, all 256 bytes; V keys
+// 32(w/2)..32(w/2)+31, head_dim columns 64(w%2)..64(w%2)+63; see issue_tile_part), so it
+// may run after the tile's last barrier, just before this wave refills the stage.
+__device__ __forceinline__ void write_pool_wave(const Params& p, const char* stage, int b,
+                                                int kvh, int k0, int w, int lane) {
+  static_assert(kWaves == 4 && kKTile == 64, "wave split of the pool copy");
+  const int64_t row_stride = (int64_t)p.num_kv_heads * kHeadDim;
+  auto dst_of = [&](int slot, int ch) -> int64_t {
+    const int key = k0 + slot;
+    if (key >= p.seq_len) return -1;
+    const int lb = key / kPoolBlock;
+    if (lb >= p.max_blocks_per_seq) return -1;
+    const int64_t phys = p.block_table[(int64_t)b * p.bt_stride + lb];
+    if (phys < 0 || phys >= p.num_pool_blocks) return -1;
+    return (phys * kPoolBlock + key % kPoolBlock) * row_stride + (int64_t)kvh * kHeadDim + 8 * ch;
+  };
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int f = 64 * j + lane;
+    {
+      const int slot = 16 * w + (f >> 4), ch = f & 15;
+      const int64_t dst = dst_of(slot, ch);
+      if (dst >= 0) *(u32x4*)(p.k_cache + dst) = *(const u32x4*)(stage + k_off(slot, ch));
+    }
+    {
+      const int slot = 32 * (w >> 1) + (f >> 3), ch = 8 * (w & 1) + (f & 7);
+      const int64_t dst = dst_of(slot, ch);
+      if (dst >= 0)
+        *(u32x4*)(p.v_cache + dst) = *(const u32x4*)(stage + kTileBytes + v_off(slot, ch));
+    }
+  }
+}
+
 // V^T MFMA fragment half: lane (col = i, g) receives keys key0 + j (j = 0..3) of head_dim
 // column 16*dt + i, where key0 = row0 + 4g.  Lane i of each 16-lane group addresses row
 // row0 + 4g + i/4, columns 16*dt + 4*(i%4)..+3 (ds_read_b64_tr_b16 hands element i%4 of
@@ -420,16 +454,22 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(Params p) {
   // previous barrier), then wait for this wave's copies and barrier.  Tile 0 is the
   // diagonal tile (masked; copied to the pool when one is given), the others lie wholly
   // below the diagonal.
+  // Both stages are free at the start: the copies of tiles 0 and 1 go out back to back,
+  // and the first wait covers tile 0 only (loads complete in issue order).
   issue_tile(p, kr, vr, st0, key0(0), w, lane);
-  wait_vmcnt<0>();
-  __builtin_amdgcn_s_barrier();
   issue_tile(p, kr, vr, st1, key0(1), w, lane);
-  if (pool) write_pool(p, st0, b, kvh, key0(0), tid);
+  wait_vmcnt<kIssuePerTile>();
+  __builtin_amdgcn_s_barrier();
+  // The pool copy of the diagonal tile: with a following tile, each wave stores its share
+  // at the start of tile 1, just before refilling stage 0, so the stores drain under tile
+  // 1's work instead of under this tile's closing wait.
+  if (pool && n == 1) write_pool(p, st0, b, kvh, key0(0), tid);
   consume_diag<HPW>(p, st0, key0(0), qpos, wave_last, col, g, qf, m_run, l_run, acc);
   wait_vmcnt<0>();
   __builtin_amdgcn_s_barrier();
 #define FI_PREFILL_STEP(IDX, CUR, NXT)                                                    \
   {                                                                                       \
+    if (pool && (IDX) == 1) write_pool_wave(p, NXT, b, kvh, key0(0), w, lane);             \
     consume_full<HPW>(p, CUR, col, g, qf, m_run, l_run, acc, kr, vr, NXT, key0((IDX) + 1), \
                       w, lane);                                                           \
     wait_vmcnt<0>();                                                                      \
