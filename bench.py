@@ -293,6 +293,65 @@ def bench_decode_step_paged(torch, fi, timer, steps, warmup, dev):
     return dict(t=t, bytes=nbytes, gbs=nbytes / t / 1e9, tok_s=B / t, tokens=sum(mid))
 
 
+def bench_decode_step_b1_graph(torch, fi, timer, steps, warmup, dev):
+    """A batch-1 decode step over 28 layers, as single-stream serving runs it: per layer the
+    fused RMSNorm + INT4 QKV projection, the fused RoPE + pool write, paged attention over a
+    1024-token context and the INT4 O projection (364 MB of packed weights).  Timed as eager
+    calls and as one HIP graph replay of the whole step (captured once; the graph removes
+    the host's per-launch cost, which dominates at batch 1)."""
+    L, B, ctx = 28, 1, 1024
+    NQKV, K_HID = (HQ + 2 * HKV) * D, HQ * D
+    g = torch.Generator(device=dev).manual_seed(11)
+    layers = []
+    for _ in range(L):
+        wqkv = (torch.randn(NQKV, K_HID, device=dev, generator=g) * 0.02).half()
+        wo = (torch.randn(K_HID, K_HID, device=dev, generator=g) * 0.02).half()
+        layers.append((fi.quantize_int4_groupwise(wqkv), fi.quantize_int4_groupwise(wo)))
+        del wqkv, wo
+    norm_w = (1.0 + 0.1 * torch.randn(K_HID, device=dev, generator=g)).half()
+    nblk = ctx // BS + 1
+    kpool = torch.randn(L, nblk, BS, HKV, D, device=dev, generator=g, dtype=torch.float16)
+    vpool = torch.randn_like(kpool)
+    table = torch.randperm(nblk, generator=torch.Generator().manual_seed(11)).int()
+    table = table.view(1, nblk).to(dev)
+    cl = torch.tensor([ctx], dtype=torch.int32, device=dev)
+    pos = torch.tensor([ctx - 1], dtype=torch.int32, device=dev)
+    cos, sin = fi.precompute_freqs(D, 4096, device=dev)
+    cos, sin = cos.half(), sin.half()
+    ws = fi.paged_attention_workspace(B, HQ, HKV, ctx, D, dev)
+    q_buf = torch.empty(B, 1, HQ, D, device=dev, dtype=torch.float16)
+    x = torch.randn(B, K_HID, device=dev, generator=g).half()
+
+    def step():
+        h = x
+        for layer in range(L):
+            wqkv, wo = layers[layer]
+            qkv = fi.rms_norm_int4_matmul(h, norm_w, wqkv)
+            q = qkv[:, :HQ * D].view(B, 1, HQ, D)
+            k = qkv[:, HQ * D:(HQ + HKV) * D].view(B, 1, HKV, D)
+            v = qkv[:, (HQ + HKV) * D:].view(B, 1, HKV, D)
+            fi.rope_store_kv(q, k, v, cos, sin, 0, kpool[layer], vpool[layer], table,
+                             start_positions=pos, return_k=False, q_out=q_buf)
+            attn = fi.paged_attention(q_buf[:, 0], kpool[layer], vpool[layer], table, BS, ctx,
+                                      context_lens=cl, workspace=ws)
+            h = fi.int4_matmul(attn.view(B, HQ * D), wo)
+        return h
+
+    n_steps, n_warm = max(1, steps // 5), max(1, warmup // 2)
+    t_eager = timer.run(step, n_steps, n_warm)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    t_graph = timer.run(graph.replay, n_steps, n_warm)
+    return dict(t_eager=t_eager, t_graph=t_graph, layers=L, ctx=ctx)
+
+
 def bench_int4(torch, fi, timer, steps, warmup, dev):
     """INT4 QKV (N 5120) and O (N 3072) projections, K 3072, over 28 layers' weights (364
     MB packed, past the 256 MB last-level cache): decode at batch 64 and batch 1, and
@@ -511,6 +570,16 @@ def main():
             "context_tokens": f["tokens"]}
         print(f"[bench] 28-layer b64 paged step (append + rope + attention): "
               f"{f['t'] * 1e3:.3f} ms, {f['gbs']:.0f} GB/s", file=sys.stderr, flush=True)
+        del f
+        gb = bench_decode_step_b1_graph(torch, fi, timer, steps, warm, dev)
+        out["decode_step_28layer_b1_graph"] = {
+            "workload": "batch-1 decode step over 28 layers: fused RMSNorm + INT4 QKV, fused "
+                        "RoPE + pool write, paged attention over 1024 tokens, INT4 O projection",
+            "eager_ms": round(gb["t_eager"] * 1e3, 4),
+            "graph_ms": round(gb["t_graph"] * 1e3, 4),
+            "graph_tokens_per_s": round(1.0 / gb["t_graph"], 1)}
+        print(f"[bench] 28-layer b1 decode step: eager {gb['t_eager'] * 1e3:.3f} ms, "
+              f"HIP graph {gb['t_graph'] * 1e3:.3f} ms", file=sys.stderr, flush=True)
 
     if "rope" in only:
         rp = bench_rope(torch, fi, timer, steps, warm, dev, 4, 4096, 0, 256, True)
