@@ -2,8 +2,8 @@
 
 Two layers of a decode step are captured once with ``torch.cuda.graph`` and replayed
 several times, with other GPU work and host synchronisation between the replays:
-  - the INT4 QKV projection (one-pass kernel at 8 rows, split-K GEMM plus reduction at
-    64 rows);
+  - RMSNorm fused with the INT4 QKV projection (one-pass kernel at 8 rows; a norm pass,
+    then split-K GEMM plus reduction at 64 rows);
   - the fused RoPE + pool write at per-row positions;
   - paged attention over per-row lengths;
   - the INT4 O projection.
@@ -12,6 +12,9 @@ Each replay must equal the eager step bit for bit: the same kernels on the same 
 rewriting the same pool slots. None of these entry points records a memset or allocates
 inside the library. The caller's caches (INT4 workspace, decode workspace) are set up by
 an eager call before capture.
+
+A captured ``PagedKVCache.append`` advances the device allocator once per replay, exactly
+as the same number of eager appends on a twin cache does.
 """
 
 import numpy as np
@@ -44,18 +47,19 @@ def _setup(B, seed):
         weights.append((quantize_int4_groupwise(wqkv), quantize_int4_groupwise(wo)))
     cos, sin = precompute_freqs(D, 4096)
     x = torch.randn(B, 3072, device=DEV, generator=g).half()
+    norm_w = (1.0 + 0.1 * torch.randn(3072, device=DEV, generator=g)).half()
     return dict(lens=lens, pos=(lens - 1).contiguous(), table=table, pools=pools, weights=weights,
-                cos=cos.half().to(DEV), sin=sin.half().to(DEV), x=x)
+                cos=cos.half().to(DEV), sin=sin.half().to(DEV), x=x, norm_w=norm_w)
 
 
 def _step(st, x, ws):
-    from fast_infer_amd import int4_matmul, paged_attention, rope_store_kv
+    from fast_infer_amd import int4_matmul, paged_attention, rms_norm_int4_matmul, rope_store_kv
 
     B = x.shape[0]
     for layer in range(L):
         wqkv, wo = st["weights"][layer]
         kc, vc = st["pools"][layer]
-        qkv = int4_matmul(x, wqkv)
+        qkv = rms_norm_int4_matmul(x, st["norm_w"], wqkv)
         q = qkv[:, :HQ * D].view(B, 1, HQ, D)
         k = qkv[:, HQ * D:(HQ + HKV) * D].view(B, 1, HKV, D)
         v = qkv[:, (HQ + HKV) * D:].view(B, 1, HKV, D)
@@ -107,3 +111,30 @@ def test_decode_step_graph_replay(hip, B):
         for (k, v), (rk, rv) in zip(st["pools"], ref_pools):
             assert torch.equal(k, rk) and torch.equal(v, rv), rep
         assert torch.isfinite(noise)
+
+
+def test_block_manager_append_graph_replay(hip):
+    banner("graph capture of PagedKVCache.append")
+    from fast_infer_amd import PagedKVCache
+
+    B = 16
+    a = PagedKVCache(1, 8, 128, 2048, 64, DEV, max_batch=B, num_blocks=400)
+    b = PagedKVCache(1, 8, 128, 2048, 64, DEV, max_batch=B, num_blocks=400)
+    lens0 = torch.randint(0, 700, (B,), generator=torch.Generator().manual_seed(3)).int()
+    a.append(lens0.to(DEV))
+    b.append(lens0.to(DEV))
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        starts_g, lens_g = a.append(1)  # recorded, not run
+    torch.cuda.synchronize()
+    assert torch.equal(a.seq_lens, b.seq_lens)
+    for rep in range(5):
+        graph.replay()
+        sb, lb = b.append(1)
+        torch.cuda.synchronize()
+        assert torch.equal(starts_g, sb) and torch.equal(lens_g, lb), rep
+        assert torch.equal(a.block_table, b.block_table), rep
+        assert torch.equal(a.seq_lens, b.seq_lens) and torch.equal(a.num_alloc, b.num_alloc), rep
+        assert torch.equal(a.free_queue, b.free_queue) and torch.equal(a.state, b.state), rep
+    a.check()
