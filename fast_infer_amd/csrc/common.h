@@ -41,6 +41,51 @@ __device__ __forceinline__ floatx4 mfma16x16x32(half8 a, half8 b, floatx4 c) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Raw buffer descriptor (stride 0, 32-bit format, no swizzle) over `num_records` bytes at
+// `base`, as four scalar words for the inline-asm copies below.
+typedef int rsrc_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ rsrc_t raw_rsrc(const void* base, int num_records) {
+  const uint64_t a = (uint64_t)(uintptr_t)base;
+  return rsrc_t{(int)(uint32_t)a, (int)(uint32_t)(a >> 32) & 0xffff, num_records, 0x00020000};
+}
+
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+
+// One direct-to-LDS copy: each lane's 16 bytes at buffer offset voffset + soffset go to LDS
+// byte lds + 16 * lane (buffer_load_dwordx4 ... lds; out-of-range lanes write zeros).  Issued
+// through inline asm so the compiler does not track it: it cannot prove later LDS reads
+// disjoint from an outstanding copy and would wait for every copy in flight before each of
+// them, which undoes any copy-ahead pipeline.  Callers order these copies themselves, with
+// wait_vmcnt and barriers; the "memory" clobber keeps other memory accesses from moving
+// across them.  M0 is set here and used by nothing else in the kernels that call this.
+__device__ __forceinline__ void lds_copy16(rsrc_t rsrc, uint32_t lds, int voffset, int soffset) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(lds), "v"(voffset), "s"(rsrc), "s"(soffset)
+               : "memory");
+}
+
+// lds_copy16 with the non-temporal (streaming) cache policy, for data read once.
+__device__ __forceinline__ void lds_copy16_nt(rsrc_t rsrc, uint32_t lds, int voffset,
+                                              int soffset) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen nt lds"
+               :
+               : "s"(lds), "v"(voffset), "s"(rsrc), "s"(soffset)
+               : "memory");
+}
+
+// Wait until at most N of this wave's vector-memory operations are outstanding (vmcnt
+// only; LDS and export counters untouched).  The kernels that stage through direct-to-LDS
+// loads count their own copies: loads complete in issue order.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
 // Cross-lane max/sum over the four 16-lane rows of a wave (lanes l, l^16, l^32, l^48).
 __device__ __forceinline__ float row4_max(float x) {
   x = fmaxf(x, __shfl_xor(x, 16));

@@ -88,14 +88,6 @@ __device__ __forceinline__ int v_off(int r, int ch) {
   return (ch >> 1) * kVPanel + r * 32 + ((ch & 1) << 4);
 }
 
-// Wait until at most `n` of this wave's vector-memory operations are outstanding
-// (vmcnt only; LDS and export counters untouched).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-
 // Issue the direct-to-LDS loads of this wave's share of the K/V tile at key k0 into
 // `stage` (K at +0, V at +kTileBytes).  One instruction moves 64 lanes x 16 bytes to
 // 1 KiB of consecutive LDS: for K, 16 keys of one panel (lane l: key l/4, chunk

@@ -33,10 +33,8 @@ constexpr int kMaxSplitTokens = 4096;                       // cap on the partit
 constexpr int kMaxSplitEntries = kMaxSplitTokens / 16 + 1;  // table entries of a partition
 constexpr int kMaxSplits = 1024;                            // partitions per row
 constexpr int kOutOfRange = 0x40000000;  // buffer offset beyond any block: loads return 0
-constexpr int kBufferWord3 = 0x00020000;  // raw buffer: 32-bit data format, no swizzle
-// Cache policy of the K/V loads: non-temporal (each byte is read once per call; not
-// allocating it in L2 streams measurably faster than default-policy loads).
-constexpr int kStreamPolicy = 2;
+// The K/V loads use the non-temporal cache policy (lds_copy16_nt): each byte is read once per
+// call, and not allocating it in L2 streams measurably faster than default-policy loads.
 
 // the wave merge reuses one tile buffer array: [wave][head][128] fp32
 static_assert(kWaves * kMaxHeadsPerWg * kHeadDim * 4 <= kWaves * kBufBytes,
@@ -78,12 +76,11 @@ __device__ __forceinline__ int row_context(const Params& p, int b) {
 
 // Buffer descriptor covering one kv head's rows of one pool block; a block outside the
 // pool gets zero records, so every load through it returns 0 without touching memory.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t block_rsrc(const half_t* pool, int64_t phys,
-                                                            int64_t block_bytes, int kv_off) {
+__device__ __forceinline__ rsrc_t block_rsrc(const half_t* pool, int64_t phys,
+                                            int64_t block_bytes, int kv_off) {
   const bool ok = phys >= 0;
   const char* base = (const char*)pool + (ok ? phys * block_bytes : 0) + kv_off;
-  return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0,
-                                           ok ? (int)(block_bytes - kv_off) : 0, kBufferWord3);
+  return raw_rsrc(base, ok ? (int)(block_bytes - kv_off) : 0);
 }
 
 // LDS tile layout: 16 rows (tokens) of 256 bytes.  K row r keeps 16-byte chunk c at slot
@@ -101,11 +98,11 @@ __device__ __forceinline__ bool issue_tile(const Params& p, const int* s_tab, in
                                            int tile, int split_end, int kv_off,
                                            int64_t block_bytes, int row_bytes, char* buf,
                                            int lane) {
-  typedef void __attribute__((address_space(3))) lds_void;
   int64_t phys = -1;
   if (tile < split_end) phys = __builtin_amdgcn_readfirstlane(s_tab[tile / p.block_size - tab0]);
-  const __amdgpu_buffer_rsrc_t kr = block_rsrc(p.k_cache, phys, block_bytes, kv_off);
-  const __amdgpu_buffer_rsrc_t vr = block_rsrc(p.v_cache, phys, block_bytes, kv_off);
+  const rsrc_t kr = block_rsrc(p.k_cache, phys, block_bytes, kv_off);
+  const rsrc_t vr = block_rsrc(p.v_cache, phys, block_bytes, kv_off);
+  const uint32_t lds = lds_addr(buf);
   const int slot0 = tile % p.block_size;  // 16-token tiles never straddle a block
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
@@ -115,21 +112,12 @@ __device__ __forceinline__ bool issue_tile(const Params& p, const int* s_tab, in
     const int vc = (lane & 15) ^ ((row & 7) << 1);
     const int koff = in ? (slot0 + row) * row_bytes + (kc << 4) : kOutOfRange;
     const int voff = in ? (slot0 + row) * row_bytes + (vc << 4) : kOutOfRange;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (lds_void*)(buf + q * 1024), 16, koff, 0, 0,
-                                             kStreamPolicy);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, (lds_void*)(buf + kTileBytes + q * 1024), 16,
-                                             voff, 0, 0, kStreamPolicy);
+    lds_copy16_nt(kr, lds + q * 1024, koff, 0);
+    lds_copy16_nt(vr, lds + kTileBytes + q * 1024, voff, 0);
   }
   return phys >= 0;
 }
 constexpr int kIssuePerTile = 8;  // load instructions per issue_tile
-
-// Wait until at most N of this wave's vector-memory operations are outstanding.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
 
 // Online-softmax update with one resident 16-token tile at `tile`.
 __device__ __forceinline__ void consume_tile(const Params& p, const char* buf, bool ok, int tile,
@@ -219,6 +207,26 @@ __global__ __launch_bounds__(256, 2) void partition_kernel(Params p) {
     }
   }
 
+  __syncthreads();
+
+  const int row_bytes = p.num_kv_heads * kHeadDim * 2;  // one pool slot, all kv heads
+  const int64_t block_bytes = (int64_t)p.block_size * row_bytes;
+  const int kv_off = kvh * kHeadDim * 2;
+  char* wb0 = buf0 + w * kBufBytes;
+  char* wb1 = buf1 + w * kBufBytes;
+
+  // Wave w takes tiles w, w + kWaves, ... of the partition, double-buffered: the copy of
+  // tile k+1 is in flight while tile k is consumed, and a buffer is refilled (tile k+2)
+  // as soon as its tile is consumed.  The first two copies go out before the Q loads.
+  const int first = split_start + w * kTileTokens;
+  const int n_t = first < split_end ? (split_end - first + kWgTokens - 1) / kWgTokens : 0;
+  bool ok0 = false, ok1 = false;
+  if (n_t > 0)
+    ok0 = issue_tile(p, s_tab, tab0, first, split_end, kv_off, block_bytes, row_bytes, wb0, lane);
+  if (n_t > 1)
+    ok1 = issue_tile(p, s_tab, tab0, first + kWgTokens, split_end, kv_off, block_bytes,
+                     row_bytes, wb1, lane);
+
   // Q^T fragments (B operand of S^T = K * Q^T): column `col` is query head head0+col;
   // MFMA i takes head_dim d = 32*i + 8*g + s in reduction slot 8*g + s (the K
   // fragment uses the same map).
@@ -233,13 +241,11 @@ __global__ __launch_bounds__(256, 2) void partition_kernel(Params p) {
       qf[i] = as_half8(v);
     }
   }
-  __syncthreads();
-
-  const int row_bytes = p.num_kv_heads * kHeadDim * 2;  // one pool slot, all kv heads
-  const int64_t block_bytes = (int64_t)p.block_size * row_bytes;
-  const int kv_off = kvh * kHeadDim * 2;
-  char* wb0 = buf0 + w * kBufBytes;
-  char* wb1 = buf1 + w * kBufBytes;
+  // The compiler does not see the tile copies (inline asm), so it would guard the first use
+  // of qf inside the loop with a wait for every outstanding load, on every iteration.  One
+  // explicit wait here (the first two tiles were issued just before) leaves it nothing to
+  // guard.
+  wait_vmcnt<0>();
 
   float m_run = kNegBig;
   float l_run = 0.f;
@@ -247,22 +253,8 @@ __global__ __launch_bounds__(256, 2) void partition_kernel(Params p) {
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) acc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  // Wave w takes tiles w, w + kWaves, ... of the partition, double-buffered: the copy of
-  // tile k+1 is in flight while tile k is consumed.
-  const int first = split_start + w * kTileTokens;
-  const int n_t = first < split_end ? (split_end - first + kWgTokens - 1) / kWgTokens : 0;
-  bool ok0 = false, ok1 = false;
-  if (n_t > 0)
-    ok0 = issue_tile(p, s_tab, tab0, first, split_end, kv_off, block_bytes, row_bytes, wb0, lane);
   for (int k = 0; k < n_t; k += 2) {
     const int t0 = first + k * kWgTokens;
-    if (k + 1 < n_t) {
-      ok1 = issue_tile(p, s_tab, tab0, t0 + kWgTokens, split_end, kv_off, block_bytes, row_bytes,
-                       wb1, lane);
-      wait_vmcnt<kIssuePerTile>();
-    } else {
-      wait_vmcnt<0>();
-    }
     consume_tile(p, wb0, ok0, t0, split_end, qf, col, g, m_run, l_run, acc);
     if (k + 1 >= n_t) break;
     if (k + 2 < n_t) {
@@ -273,6 +265,14 @@ __global__ __launch_bounds__(256, 2) void partition_kernel(Params p) {
       wait_vmcnt<0>();
     }
     consume_tile(p, wb1, ok1, t0 + kWgTokens, split_end, qf, col, g, m_run, l_run, acc);
+    if (k + 2 >= n_t) break;
+    if (k + 3 < n_t) {
+      ok1 = issue_tile(p, s_tab, tab0, t0 + 3 * kWgTokens, split_end, kv_off, block_bytes,
+                       row_bytes, wb1, lane);
+      wait_vmcnt<kIssuePerTile>();
+    } else {
+      wait_vmcnt<0>();
+    }
   }
 
   l_run = row4_sum(l_run);
