@@ -309,6 +309,141 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(Params p) {
   store_tile<kMSub>(p, acc, m0, blockIdx.x * kNTile);
 }
 
+// ---------------------------------------------------------------------------------------
+// Packed-weight GEMM for 17..64 rows, staged through direct-to-LDS copies.  The tile and
+// MFMA layout are gemm_kernel's (64 columns x MT rows per workgroup, 16 columns per wave,
+// one 128-wide K group per step), but each group's X tile (MT rows x 256 bytes) and W tile
+// (64 rows x 64 bytes) are copied global -> LDS with `buffer_load ... lds` into a ring of
+// three stages, two groups ahead of the MFMAs.  The copies hold no registers, so two
+// groups stay in flight while a third is multiplied; gemm_kernel keeps one group ahead in
+// registers and waits out most of a memory latency per group.
+//
+// X rows sit in LDS unpadded, their 16-byte chunks XOR-permuted by row % 16 (the copy
+// lane that fills slot c of row r fetches chunk c ^ (r % 16)), so the 16 rows one MFMA
+// operand read touches fall on distinct banks.  X rows past M and weight rows past N read
+// zeros through the buffer bounds check.  The group scales of the workgroup's 64 columns
+// are staged in LDS once, at the start.
+constexpr int kDmaStages = 3;
+constexpr int kDmaMaxGroups = 64;  // K groups per workgroup (one K split) the scale table holds
+
+template <int MT>
+struct DmaTile {
+  static constexpr int kXBytes = MT * 256;             // X tile of one group
+  static constexpr int kWBytes = kNTile * 64;          // W tile of one group (4 KiB)
+  static constexpr int kStage = kXBytes + kWBytes;
+  static constexpr int kXPerWave = kXBytes / 1024 / 4;  // X copies per wave per group
+  static constexpr int kIssue = kXPerWave + 1;          // copies per wave per group
+};
+
+// This wave's copies of group g into `stage`: X slots wave * kXPerWave + q (1 KiB each,
+// X rows 4i..4i+3 of slot i) and W rows 16 * wave .. + 15.
+template <int MT>
+__device__ __forceinline__ void dma_issue(rsrc_t xr, rsrc_t wr, char* stage, int g,
+                                          const int (&xoff)[DmaTile<MT>::kXPerWave], int woff,
+                                          int wave) {
+  using T = DmaTile<MT>;
+  const uint32_t base = lds_addr(stage);
+#pragma unroll
+  for (int q = 0; q < T::kXPerWave; ++q)
+    lds_copy16(xr, base + (wave * T::kXPerWave + q) * 1024, xoff[q], g * 256);
+  lds_copy16(wr, base + T::kXBytes + wave * 1024, woff, g * (kGroup / 2));
+}
+
+// One group's MFMAs from a resident stage: this lane's 16 weight bytes (k = 32 grp ..
+// +31 of its column) dequantized with the group's scale, against X rows 16 j + row.
+template <int MT>
+__device__ __forceinline__ void dma_group(const char* stage, const half_t* sc, int t, int wave,
+                                          int row, int grp, floatx4 (&acc)[MT / 16]) {
+  using T = DmaTile<MT>;
+  const u32x4 wv = *(const u32x4*)(stage + T::kXBytes + wave * 1024 + row * 64 + grp * 16);
+  const half_t s = sc[(16 * wave + row) * kDmaMaxGroups + t];
+  const half2_t s2 = {s, s};
+  half8 wf[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) wf[k] = dequant8(wv[k], s2);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int chunk = ((4 * grp + k) ^ row) << 4;
+#pragma unroll
+    for (int j = 0; j < MT / 16; ++j) {
+      const u32x4 xv = *(const u32x4*)(stage + (16 * j + row) * 256 + chunk);
+      acc[j] = mfma16x16x32(wf[k], as_half8(xv), acc[j]);
+    }
+  }
+}
+
+template <int MT>
+__global__ __launch_bounds__(kThreads, 2) void gemm_dma_kernel(Params p) {
+  using T = DmaTile<MT>;
+  constexpr int kMSub = MT / 16;
+  // the ring's stages are distinct objects, so the compiler tracks each one's copies apart
+  __shared__ __attribute__((aligned(16))) char st0[T::kStage];
+  __shared__ __attribute__((aligned(16))) char st1[T::kStage];
+  __shared__ __attribute__((aligned(16))) char st2[T::kStage];
+  __shared__ half_t sc[kNTile * kDmaMaxGroups];
+  static_assert(kDmaStages == 3, "the step macro below rotates three stages");
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int row = lane & 15;
+  const int grp = lane >> 4;
+  const int n0 = blockIdx.x * kNTile;
+  const int m0 = blockIdx.y * MT;
+  const int groups = p.K / kGroup;
+  const int g_begin = blockIdx.z * p.groups_per_split;
+  const int G = min(g_begin + p.groups_per_split, groups) - g_begin;  // <= 0: nothing to add
+
+  for (int f = threadIdx.x; f < kNTile * G; f += kThreads) {
+    const int col = f / G, t = f - col * G;
+    const int n = min(n0 + col, p.N - 1);
+    sc[col * kDmaMaxGroups + t] = p.scales[(int64_t)n * p.s_stride + g_begin + t];
+  }
+  __syncthreads();
+
+  const int rows_x = min(MT, p.M - m0);
+  const int rows_w = min(kNTile, p.N - n0);
+  const rsrc_t xr =
+      raw_rsrc(p.x + (int64_t)m0 * p.x_stride, (int)((rows_x - 1) * p.x_stride * 2 + p.K * 2));
+  const rsrc_t wr = raw_rsrc(p.w + (int64_t)n0 * p.w_stride, (int)((rows_w - 1) * p.w_stride + p.K / 2));
+  int xoff[T::kXPerWave];
+#pragma unroll
+  for (int q = 0; q < T::kXPerWave; ++q) {
+    const int r = 4 * (wave * T::kXPerWave + q) + (lane >> 4);
+    xoff[q] = r * (int)p.x_stride * 2 + (((lane & 15) ^ (r & 15)) << 4);
+  }
+  const int woff = (16 * wave + (lane >> 2)) * (int)p.w_stride + (lane & 3) * 16;
+
+  floatx4 acc[kMSub];
+#pragma unroll
+  for (int j = 0; j < kMSub; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  if (G > 0) dma_issue<MT>(xr, wr, st0, g_begin, xoff, woff, wave);
+  if (G > 1) dma_issue<MT>(xr, wr, st1, g_begin + 1, xoff, woff, wave);
+  // Step t: wait for group t's copies (group t + 1's may still be in flight), barrier (so
+  // every wave's copies of group t have landed and every wave is done with group t - 1's
+  // stage), refill that stage with group t + 2, multiply group t.
+#define FI_DMA_STEP(TT, CUR, NXT)                                                 \
+  {                                                                               \
+    if ((TT) + 1 < G)                                                             \
+      wait_vmcnt<T::kIssue>();                                                    \
+    else                                                                          \
+      wait_vmcnt<0>();                                                            \
+    __builtin_amdgcn_s_barrier();                                                 \
+    if ((TT) + 2 < G) dma_issue<MT>(xr, wr, NXT, g_begin + (TT) + 2, xoff, woff, wave); \
+    dma_group<MT>(CUR, sc, (TT), wave, row, grp, acc);                            \
+  }
+  for (int t = 0; t < G; t += 3) {
+    FI_DMA_STEP(t, st0, st2)
+    if (t + 1 >= G) break;
+    FI_DMA_STEP(t + 1, st1, st0)
+    if (t + 2 >= G) break;
+    FI_DMA_STEP(t + 2, st2, st1)
+  }
+#undef FI_DMA_STEP
+
+  store_tile<kMSub>(p, acc, m0, n0);
+}
+
 // Prefill-sized calls: the MFMA kernels above spend most of their time dequantizing (each
 // weight is dequantized once per row tile) at these sizes, so the weight is dequantized once
 // into the workspace and the plain fp16 GEMM runs in rocBLAS (fp16 in and out, fp32
@@ -638,6 +773,18 @@ int check_linear(const char* fn, const void* x, int64_t x_stride, int64_t M, int
   return FI_OK;
 }
 
+// Packed weights at 17..64 rows go through gemm_dma_kernel when its scale table holds a
+// split's groups and its 32-bit copy offsets cover the operands.  FI_INT4_DMA=0 keeps
+// gemm_kernel (tuning).
+bool dma_ok(const fi::gemm::Params& p, const fi::gemm::Plan& pl) {
+  using namespace fi::gemm;
+  static const int env = env_int("FI_INT4_DMA", 1);
+  if (!env || (pl.mt != 32 && pl.mt != 64) || p.groups_per_split > kDmaMaxGroups) return false;
+  const int64_t x_span = (int64_t)pl.mt * p.x_stride * 2 + (int64_t)p.K * 2;
+  const int64_t w_span = (int64_t)kNTile * p.w_stride + p.K / 2;
+  return x_span < (1ll << 31) - 4096 && w_span < (1ll << 31) - 4096;
+}
+
 // kNorm: the RMSNorm is fused into the decode kernel (only on the gemv path).
 template <bool kNorm>
 void launch_linear(const fi::gemm::Params& base, bool int4, const fi::gemm::Plan& pl,
@@ -667,11 +814,18 @@ void launch_linear(const fi::gemm::Params& base, bool int4, const fi::gemm::Plan
     else                                                                                    \
       hipLaunchKernelGGL((gemm_kernel<MT, false>), grid, dim3(kThreads), 0, st, p);          \
   } while (0)
-  switch (pl.mt) {
-    case 16: FI_GEMM_LAUNCH(16); break;
-    case 32: FI_GEMM_LAUNCH(32); break;
-    case 64: FI_GEMM_LAUNCH(64); break;
-    default: FI_GEMM_LAUNCH(128); break;
+  if (int4 && dma_ok(p, pl)) {
+    if (pl.mt == 32)
+      hipLaunchKernelGGL(gemm_dma_kernel<32>, grid, dim3(kThreads), 0, st, p);
+    else
+      hipLaunchKernelGGL(gemm_dma_kernel<64>, grid, dim3(kThreads), 0, st, p);
+  } else {
+    switch (pl.mt) {
+      case 16: FI_GEMM_LAUNCH(16); break;
+      case 32: FI_GEMM_LAUNCH(32); break;
+      case 64: FI_GEMM_LAUNCH(64); break;
+      default: FI_GEMM_LAUNCH(128); break;
+    }
   }
 #undef FI_GEMM_LAUNCH
   if (pl.splits > 1) {
