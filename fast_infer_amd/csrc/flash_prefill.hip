@@ -134,24 +134,32 @@ __device__ __forceinline__ void issue_tile(const Params& p, __amdgpu_buffer_rsrc
 }
 constexpr int kIssuePerTile = 2 * (kTileBytes / 1024) / kWaves;  // DMA instructions per wave per tile
 
-// Copy a resident tile (keys k0..k0+kKTile-1, whole pool blocks of 64) from LDS into
-// the pool.
+// The diagonal tile (keys k0 .. k0 + 63, k0 a multiple of 64) is exactly one pool block:
+// logical block k0 / 64 of the row, whose table entry `entry` the caller loaded (valid only
+// when `row_ok`, i.e. that block is inside the table).  The entry is passed through an
+// empty asm statement first, so its first use (and the compiler's wait for the load) stays
+// here, after the caller's own waits, rather than next to the load.
+__device__ __forceinline__ int64_t pool_block_base(const Params& p, bool row_ok, int entry,
+                                                   int kvh) {
+  asm volatile("" : "+v"(entry));
+  entry = __builtin_amdgcn_readfirstlane(entry);
+  if (!row_ok || entry < 0 || entry >= p.num_pool_blocks) return -1;
+  return (int64_t)entry * kPoolBlock * p.num_kv_heads * kHeadDim + (int64_t)kvh * kHeadDim;
+}
+
+// Copy the resident diagonal tile from LDS into its pool block.
 template <int NT = kThreads>
-__device__ __forceinline__ void write_pool(const Params& p, const char* stage, int b, int kvh,
-                                           int k0, int tid) {
+__device__ __forceinline__ void write_pool(const Params& p, const char* stage, bool row_ok,
+                                           int entry, int kvh, int k0, int tid) {
+  const int64_t base = pool_block_base(p, row_ok, entry, kvh);
+  if (base < 0) return;
   const int64_t row_stride = (int64_t)p.num_kv_heads * kHeadDim;
 #pragma unroll
   for (int j = 0; j < kKTile * 16 / NT; ++j) {
     const int f = NT * j + tid;
     const int slot = f >> 4;  // row within the tile
-    const int key = k0 + slot;
-    if (key >= p.seq_len) continue;
-    const int lb = key / kPoolBlock;
-    if (lb >= p.max_blocks_per_seq) continue;
-    const int64_t phys = p.block_table[(int64_t)b * p.bt_stride + lb];
-    if (phys < 0 || phys >= p.num_pool_blocks) continue;
-    const int64_t dst = (phys * kPoolBlock + key % kPoolBlock) * row_stride +
-                        (int64_t)kvh * kHeadDim + 8 * (f & 15);
+    if (k0 + slot >= p.seq_len) continue;
+    const int64_t dst = base + slot * row_stride + 8 * (f & 15);
     *(u32x4*)(p.k_cache + dst) = *(const u32x4*)(stage + k_off(slot, f & 15));
     *(u32x4*)(p.v_cache + dst) = *(const u32x4*)(stage + kTileBytes + v_off(slot, f & 15));
   }
@@ -161,32 +169,26 @@ __device__ __forceinline__ void write_pool(const Params& p, const char* stage, i
 // instructions of a later tile overwrite (K keys 16w..16w+15, all 256 bytes; V keys
 // 32(w/2)..32(w/2)+31, head_dim columns 64(w%2)..64(w%2)+63; see issue_tile_part), so it
 // may run after the tile's last barrier, just before this wave refills the stage.
-__device__ __forceinline__ void write_pool_wave(const Params& p, const char* stage, int b,
-                                                int kvh, int k0, int w, int lane) {
+__device__ __forceinline__ void write_pool_wave(const Params& p, const char* stage, bool row_ok,
+                                                int entry, int kvh, int k0, int w, int lane) {
   static_assert(kWaves == 4 && kKTile == 64, "wave split of the pool copy");
+  const int64_t base = pool_block_base(p, row_ok, entry, kvh);
+  if (base < 0) return;
   const int64_t row_stride = (int64_t)p.num_kv_heads * kHeadDim;
-  auto dst_of = [&](int slot, int ch) -> int64_t {
-    const int key = k0 + slot;
-    if (key >= p.seq_len) return -1;
-    const int lb = key / kPoolBlock;
-    if (lb >= p.max_blocks_per_seq) return -1;
-    const int64_t phys = p.block_table[(int64_t)b * p.bt_stride + lb];
-    if (phys < 0 || phys >= p.num_pool_blocks) return -1;
-    return (phys * kPoolBlock + key % kPoolBlock) * row_stride + (int64_t)kvh * kHeadDim + 8 * ch;
-  };
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int f = 64 * j + lane;
     {
       const int slot = 16 * w + (f >> 4), ch = f & 15;
-      const int64_t dst = dst_of(slot, ch);
-      if (dst >= 0) *(u32x4*)(p.k_cache + dst) = *(const u32x4*)(stage + k_off(slot, ch));
+      if (k0 + slot < p.seq_len)
+        *(u32x4*)(p.k_cache + base + slot * row_stride + 8 * ch) =
+            *(const u32x4*)(stage + k_off(slot, ch));
     }
     {
       const int slot = 32 * (w >> 1) + (f >> 3), ch = 8 * (w & 1) + (f & 7);
-      const int64_t dst = dst_of(slot, ch);
-      if (dst >= 0)
-        *(u32x4*)(p.v_cache + dst) = *(const u32x4*)(stage + kTileBytes + v_off(slot, ch));
+      if (k0 + slot < p.seq_len)
+        *(u32x4*)(p.v_cache + base + slot * row_stride + 8 * ch) =
+            *(const u32x4*)(stage + kTileBytes + v_off(slot, ch));
     }
   }
 }
@@ -439,6 +441,12 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(Params p) {
     return (idx == 0 ? qt : idx - 1) * kKTile;
   };
   const bool pool = p.k_cache != nullptr && hsub == 0;
+  // The pool block of the diagonal tile: logical block qt of row b.  Its table entry is
+  // loaded before the copies and first used in the pool write, so the load's latency
+  // hides under the first tile's (read only when pool_row).
+  const bool pool_row = pool && qt < p.max_blocks_per_seq;
+  int pool_entry;
+  if (pool_row) pool_entry = p.block_table[(int64_t)b * p.bt_stride + qt];
   const int wave_last = q0 + kRowsPerWave * w + kRowsPerWave - 1;  // last position of the wave
 
   // Two-stage pipeline over 128-key tiles (tile idx in stage idx % 2): while consuming
@@ -455,13 +463,13 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(Params p) {
   // The pool copy of the diagonal tile: with a following tile, each wave stores its share
   // at the start of tile 1, just before refilling stage 0, so the stores drain under tile
   // 1's work instead of under this tile's closing wait.
-  if (pool && n == 1) write_pool(p, st0, b, kvh, key0(0), tid);
+  if (pool && n == 1) write_pool(p, st0, pool_row, pool_entry, kvh, key0(0), tid);
   consume_diag<HPW>(p, st0, key0(0), qpos, wave_last, col, g, qf, m_run, l_run, acc);
   wait_vmcnt<0>();
   __builtin_amdgcn_s_barrier();
 #define FI_PREFILL_STEP(IDX, CUR, NXT)                                                    \
   {                                                                                       \
-    if (pool && (IDX) == 1) write_pool_wave(p, NXT, b, kvh, key0(0), w, lane);             \
+    if (pool && (IDX) == 1) write_pool_wave(p, NXT, pool_row, pool_entry, kvh, key0(0), w, lane); \
     consume_full<HPW>(p, CUR, col, g, qf, m_run, l_run, acc, kr, vr, NXT, key0((IDX) + 1), \
                       w, lane);                                                           \
     wait_vmcnt<0>();                                                                      \
