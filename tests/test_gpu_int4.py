@@ -85,10 +85,32 @@ def test_int4_matmul_strided_x_and_batch_dims(hip):
     g = torch.Generator().manual_seed(9)
     big = torch.randn(2, 7, K + 256, generator=g).half()
     x = big[..., 128:128 + K]                 # [2, 7, K], row stride K + 256
-    out = int4_matmul(x.to(DEV), (packed, scales))
+    xd = big.to(DEV)[..., 128:128 + K]        # the same view on the device
+    assert xd.stride(1) == K + 256
+    out = int4_matmul(xd, (packed, scales))
     assert out.shape == (2, 7, N)
     torch.cuda.synchronize()
     _check(out.reshape(14, N), x.reshape(14, K).numpy(), dequantize_int4(packed, scales).cpu().numpy())
+
+
+# 17..64 rows run the LDS-staged kernel (gemm_dma_kernel): one K group, a two-way K split
+# whose second part is shorter, an 11-way split of 64 groups, partial last column tiles,
+# strided X rows
+@pytest.mark.parametrize("M,N,K,pad", [(17, 64, 128, 0), (20, 130, 640, 0), (40, 70, 8192, 264),
+                                       (64, 200, 3072, 512), (33, 5120, 3072, 8)])
+def test_int4_matmul_lds_staged_shapes(hip, M, N, K, pad):
+    banner(f"int4_matmul staged M={M} N={N} K={K} row pad {pad}")
+    from fast_infer_amd import dequantize_int4, int4_matmul, quantize_int4_groupwise
+
+    w = _weights(M + N, N, K, 0.02)
+    packed, scales = quantize_int4_groupwise(torch.from_numpy(w).to(DEV))
+    g = torch.Generator().manual_seed(M * 31 + K)
+    big = torch.randn(M, K + pad, generator=g).half()
+    xd = big.to(DEV)[:, 8:8 + K] if pad else big.to(DEV)   # row stride K + pad on the device
+    assert xd.stride(0) == K + pad
+    out = int4_matmul(xd, (packed, scales))
+    torch.cuda.synchronize()
+    _check(out, xd.cpu().numpy(), dequantize_int4(packed, scales).cpu().numpy())
 
 
 def test_int4_matmul_prefill_size_sampled(hip):
