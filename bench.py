@@ -46,10 +46,11 @@ sys.path.insert(0, str(ROOT))
 METRIC = "decode attn GB/s + prefill attn TFLOP/s (% of MI355X roofline), fp16"
 HQ, HKV, D, BS = 24, 8, 128, 64
 # MFMA-bound kernels (prefill attention, the prefill GEMM) run 10-20% slower over their
-# first few tens of milliseconds of back-to-back calls in a process (same tensors; a GEMM
-# load beforehand does not remove it); their sections keep calling, untimed, for this long
-# before timing.
-MFMA_WARM_S = 0.1
+# first few tens of milliseconds of back-to-back calls (same tensors; a GEMM load
+# beforehand does not remove it), and on a GPU that has just been idle a 0.1 s warm-up
+# still left the first process's prefill about 4% slower than a second process's; their
+# sections keep calling, untimed, for this long before timing.
+MFMA_WARM_S = 0.5
 
 
 def _args():
