@@ -442,11 +442,10 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(Params p) {
   };
   const bool pool = p.k_cache != nullptr && hsub == 0;
   // The pool block of the diagonal tile: logical block qt of row b.  Its table entry is
-  // loaded before the copies and first used in the pool write, so the load's latency
-  // hides under the first tile's (read only when pool_row).
+  // loaded right after the first copies go out and first used in the pool write, so the
+  // load's latency hides under the first tile's.
   const bool pool_row = pool && qt < p.max_blocks_per_seq;
-  int pool_entry;
-  if (pool_row) pool_entry = p.block_table[(int64_t)b * p.bt_stride + qt];
+  int pool_entry = -1;
   const int wave_last = q0 + kRowsPerWave * w + kRowsPerWave - 1;  // last position of the wave
 
   // Two-stage pipeline over 128-key tiles (tile idx in stage idx % 2): while consuming
@@ -458,6 +457,7 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(Params p) {
   // and the first wait covers tile 0 only (loads complete in issue order).
   issue_tile(p, kr, vr, st0, key0(0), w, lane);
   issue_tile(p, kr, vr, st1, key0(1), w, lane);
+  if (pool_row) pool_entry = p.block_table[(int64_t)b * p.bt_stride + qt];
   wait_vmcnt<kIssuePerTile>();
   __builtin_amdgcn_s_barrier();
   // The pool copy of the diagonal tile: with a following tile, each wave stores its share
