@@ -351,6 +351,41 @@ def test_flash_prefill_vs_reference_and_oracle(hip, golden, name, expanded):
     assert _maxabs(out.cpu(), OA.causal_attention(q, k, v)) <= ATOL
 
 
+@pytest.mark.parametrize("S,width", [(300, 3), (130, 1), (64, 1)])
+def test_flash_prefill_pool_write_partial_table(hip, S, width):
+    """A table narrower than the sequence, with a -1 entry and an entry past the pool: only
+    the blocks with valid entries are written (bit-exact), every other pool byte keeps its
+    value, and the attention output is the plain one."""
+    banner(f"flash prefill pool write, S={S}, table width {width}")
+    from fast_infer_amd import flash_attention
+
+    B, H, Hkv, N = 3, 24, 8, 12
+    g = torch.Generator().manual_seed(S + width)
+    q = torch.randn(B, S, H, 128, generator=g).half().transpose(1, 2)
+    k = torch.randn(B, S, Hkv, 128, generator=g).half().transpose(1, 2)
+    v = torch.randn(B, S, Hkv, 128, generator=g).half().transpose(1, 2)
+    table = torch.tensor([[4, 7, 1][:width], [-1, 2, 9][:width], [N + 5, 0, 3][:width]],
+                         dtype=torch.int32)
+    kc0 = torch.randn(N, 64, Hkv, 128, generator=g).half()
+    vc0 = torch.randn(N, 64, Hkv, 128, generator=g).half()
+    kc, vc = kc0.to(DEV), vc0.to(DEV)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    out = flash_attention(qd, kd, vd, k_cache=kc, v_cache=vc, block_table=table.to(DEV))
+    plain = flash_attention(qd, kd, vd)
+    torch.cuda.synchronize()
+    assert torch.equal(out, plain)
+    ek, ev = kc0.clone(), vc0.clone()
+    for b in range(B):
+        for lb in range(min(width, math.ceil(S / 64))):
+            phys = int(table[b, lb])
+            if not 0 <= phys < N:
+                continue
+            n = min(64, S - 64 * lb)
+            ek[phys, :n] = k[b, :, 64 * lb:64 * lb + n].transpose(0, 1)
+            ev[phys, :n] = v[b, :, 64 * lb:64 * lb + n].transpose(0, 1)
+    assert torch.equal(kc.cpu(), ek) and torch.equal(vc.cpu(), ev)
+
+
 @pytest.mark.parametrize("S", [64, 200, 1000])
 def test_flash_prefill_fused_pool_write(hip, S):
     banner(f"flash prefill fused pool write S={S}")
