@@ -471,9 +471,9 @@ def cpu_baseline_prefill(torch, res, cores, B, S, nprog=16):
 def main():
     a = _args()
     if a.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {a.gpus} is not supported (the attention "
-              "path runs on a single MI355X here; see DESIGN.md for how it would shard).",
-              file=sys.stderr)
+        print(f"bench.py measures one GPU; --gpus {a.gpus} is not supported: the attention "
+              "path runs on a single MI355X (a multi-GPU run would shard rows and kv heads "
+              "across GPUs, each running this same single-GPU path).", file=sys.stderr)
         sys.exit(2)
     import torch
 
