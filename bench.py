@@ -79,9 +79,15 @@ def _traffic(workload: str):
     return None
 
 
-def _cores() -> int:
-    # the GPU box grants 16 host cores per GPU whatever the affinity mask shows
-    return max(1, min(16, len(os.sched_getaffinity(0))))
+# Host threads the CPU baseline may use: a one-GPU box grants 16 host cores per GPU, which
+# the affinity mask does not necessarily show, so the thread count is capped there.
+CPU_THREAD_CAP = 16
+
+
+def _cores() -> tuple[int, int]:
+    """(threads used by the CPU baseline, cores in this process's affinity mask)."""
+    visible = len(os.sched_getaffinity(0))
+    return max(1, min(CPU_THREAD_CAP, visible)), visible
 
 
 class Timer:
@@ -487,7 +493,8 @@ def main():
     timer = Timer(torch)
     only = set(filter(None, a.only.split(","))) or {"decode", "prefill", "small", "e2e", "rope",
                                                     "int4"}
-    cores = _cores()
+    cores, cores_visible = _cores()
+    core_note = {"cores_in_affinity_mask": cores_visible, "thread_cap": CPU_THREAD_CAP}
     steps, warm = a.steps, a.warmup
     out = {"metric": METRIC}
 
@@ -640,7 +647,7 @@ def main():
                           f"kernel (oracle/ref_algo.c, OpenMP), {c['reps']} reps, "
                           f"{c['t_port'] * 1e3:.1f} ms/call",
                 "torch_fp32_oracle": {"value": round(c["torch"], 3), "unit": "GB/s",
-                                      "s_per_call": round(c["t_torch"], 3)}}
+                                      "s_per_call": round(c["t_torch"], 3)}, **core_note}
             print(f"[bench] cpu decode: port {c['port']:.2f} GB/s, torch {c['torch']:.2f} GB/s",
                   file=sys.stderr, flush=True)
         if pre is not None:
@@ -652,7 +659,8 @@ def main():
                           f"programs, extrapolated to the full call "
                           f"({c['t_port']:.1f} s/call)",
                 "torch_fp32_oracle": {"value": round(c["torch"], 4), "unit": "TFLOP/s",
-                                      "sample": "4 heads of batch row 0, extrapolated"}}
+                                      "sample": "4 heads of batch row 0, extrapolated"},
+                **core_note}
             print(f"[bench] cpu prefill: port {c['port']:.4f} TFLOP/s", file=sys.stderr,
                   flush=True)
 

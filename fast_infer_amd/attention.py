@@ -90,10 +90,11 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     num_kv_heads = k.shape[1]
     if num_kv_heads == 0 or num_heads % num_kv_heads:
         raise ValueError(f"num_heads {num_heads} is not a multiple of kv heads {num_kv_heads}")
+    o = torch.empty_like(q)  # q's strides (:99)
     q, k, v = _prep_rows(q), _prep_rows(k), _prep_rows(v)
-    o = torch.empty_like(q)
-    if not _rows_ok(o):
-        o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    # the kernel writes 16-byte rows; an output whose strides do not allow that is
+    # computed into a contiguous buffer and copied into o at the end
+    work = o if _rows_ok(o) else torch.empty(q.shape, dtype=q.dtype, device=q.device)
 
     kc = vc = bt = None
     n_pool = bt_stride = max_blocks = 0
@@ -117,16 +118,18 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         return o
     lib = _lib.load()
     rc = lib.fi_flash_attention_fwd(
-        q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), work.data_ptr(),
         batch, num_heads, num_kv_heads, seq_len, head_dim,
         q.stride(0), q.stride(1), q.stride(2),
         k.stride(0), k.stride(1), k.stride(2),
         v.stride(0), v.stride(1), v.stride(2),
-        o.stride(0), o.stride(1), o.stride(2),
+        work.stride(0), work.stride(1), work.stride(2),
         float(sm_scale),
         _ptr(kc), _ptr(vc), n_pool, block_size, _ptr(bt), bt_stride, max_blocks,
         _lib.stream_handle(q.device))
     _lib.check(rc, "flash_attention")
+    if work is not o:
+        o.copy_(work)
     return o
 
 
@@ -191,10 +194,9 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
         if context_lens.numel() < batch:
             raise ValueError("context_lens has fewer entries than the batch")
         context_lens = context_lens.contiguous()
+    o = torch.empty_like(q)  # q's strides (:216)
     q = _prep_rows(q)
-    o = torch.empty_like(q)
-    if not _rows_ok(o):
-        o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    work = o if _rows_ok(o) else torch.empty(q.shape, dtype=q.dtype, device=q.device)
     if batch == 0:
         return o
 
@@ -210,9 +212,11 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
         k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[0], block_size, num_kv_heads,
         block_table.data_ptr(), block_table.stride(0), block_table.shape[1],
         _ptr(context_lens), num_tokens,
-        o.data_ptr(), o.stride(0), o.stride(1),
+        work.data_ptr(), work.stride(0), work.stride(1),
         batch, num_q_heads, head_dim, float(sm_scale),
         ws_ptr, ws_bytes,
         _lib.stream_handle(q.device))
     _lib.check(rc, "paged_attention")
+    if work is not o:
+        o.copy_(work)
     return o

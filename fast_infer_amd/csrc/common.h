@@ -60,7 +60,11 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // disjoint from an outstanding copy and would wait for every copy in flight before each of
 // them, which undoes any copy-ahead pipeline.  Callers order these copies themselves, with
 // wait_vmcnt and barriers; the "memory" clobber keeps other memory accesses from moving
-// across them.  M0 is set here and used by nothing else in the kernels that call this.
+// across them.  M0 is set here without being declared: LLVM treats M0 as a reserved
+// register and ignores it in a clobber list, so declaring it would not make the compiler
+// save a live value.  The copies are sound only while no other instruction of the calling
+// kernels uses M0; tests/test_device_code.py checks that in the compiled code (every M0
+// write is this helper's, directly followed by its copy).
 __device__ __forceinline__ void lds_copy16(rsrc_t rsrc, uint32_t lds, int voffset, int soffset) {
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                :

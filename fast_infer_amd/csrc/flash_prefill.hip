@@ -57,6 +57,7 @@ struct Params {
   float lazy_raw;    // kLazyLog2 / scale_log2: slack of the reference max in raw units
   float lazy_log2;   // lazy_raw * scale_log2 (about kLazyLog2)
   uint32_t q_sign;   // 0x80008000 when sm_scale < 0: Q is negated instead of the scale
+  int q_rows;        // rows of Q loaded: seq_len, or 0 when sm_scale == 0 (Q read as zeros)
   int num_q_tiles;
   int k_records;     // bytes addressable from one (batch, kv head) base of k
   int v_records;
@@ -418,7 +419,7 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(Params p) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       u32x4 v = {0u, 0u, 0u, 0u};
-      if (qpos < p.seq_len) v = *(const u32x4*)(qrow + 32 * i + 8 * g);
+      if (qpos < p.q_rows) v = *(const u32x4*)(qrow + 32 * i + 8 * g);
       qf[j][i] = as_half8(v ^ p.q_sign);  // exact negation when sm_scale < 0
     }
   }
@@ -577,8 +578,13 @@ extern "C" int fi_flash_attention_fwd(const void* q, const void* k, const void* 
   p.num_kv_heads = (int)num_kv_heads;
   p.group = (int)group;
   p.hg_per_kv = (int)(group / hpw);
-  p.scale_log2 = (sm_scale < 0 ? -sm_scale : sm_scale) * kLog2e;
+  // A zero scale makes every valid score 0 (uniform weights over the causal keys).  The
+  // kernel masks scores to -inf before scaling, and -inf * 0 is NaN, so that case runs with
+  // unit scale on an all-zero Q instead: scores are exactly 0, masked ones -inf.
+  const bool zero_scale = sm_scale == 0.f;
+  p.scale_log2 = zero_scale ? kLog2e : (sm_scale < 0 ? -sm_scale : sm_scale) * kLog2e;
   p.q_sign = sm_scale < 0 ? 0x80008000u : 0u;
+  p.q_rows = zero_scale ? 0 : (int)seq_len;
   p.lazy_raw = p.scale_log2 > 0.f ? kLazyLog2 / p.scale_log2 : 0.f;
   p.lazy_log2 = p.lazy_raw * p.scale_log2;
   p.num_q_tiles = (int)((seq_len + kQTile - 1) / kQTile);

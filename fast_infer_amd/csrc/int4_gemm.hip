@@ -5,7 +5,7 @@
 // row holds k = 2j in its low nibble and k = 2j+1 in its high nibble, each a 4-bit two's
 // complement value in [-8, 7]; scales are fp16 [N, K/128], one per 128-wide group.
 // The weight the reference multiplies with is fp16(q * scale) (matmul.py:83-84 and
-// :197-214): one rounding of an exact product, which is what v_pk_mul_f16 computes.
+// :309-326): one rounding of an exact product, which is what v_pk_mul_f16 computes.
 //
 // GEMM: C[m, n] = fp16( sum_k X[m, k] * W[n, k] ), fp32 accumulation (matmul.py:14-132,
 // :135-186).  One workgroup = 4 waves = 64 output columns (16 per wave) x MT rows, over a
@@ -647,7 +647,7 @@ __global__ __launch_bounds__(256) void quantize_kernel(const half_t* w, int64_t 
   }
 }
 
-// matmul.py:197-214 (_dequant_storage): W = fp16(q * scale), 8 values per thread.
+// matmul.py:309-326 (_dequant_storage): W = fp16(q * scale), 8 values per thread.
 __global__ __launch_bounds__(256) void dequantize_kernel(const uint8_t* packed, int64_t p_stride,
                                                          const half_t* scales, int64_t s_stride,
                                                          int N, int K, half_t* w,
@@ -673,31 +673,22 @@ struct Plan {
   bool library;  // prefill-sized: dequantize once, then a plain fp16 GEMM (rocBLAS)
 };
 
-inline int gemv_limit() {
-  static int v = [] {
-    const char* e = getenv("FI_INT4_GEMV_MAX_M");
-    return e ? atoi(e) : 16;
-  }();
-  return v;
-}
-
-inline int env_int(const char* name, int dflt) {
-  const char* e = getenv(name);
-  return e ? atoi(e) : dflt;
-}
+// Dispatch thresholds (rows of X), chosen by measurement on MI355X: the one-pass kernel
+// up to 16 rows, the tiled split-K kernels up to 128, the library GEMM above.
+constexpr int kGemvMaxM = 16;
+constexpr int kLibraryMinM = 129;
 
 inline Plan plan(int64_t M, int64_t N, int64_t K) {
   Plan pl;
   pl.gemv_rows = 0;
   pl.library = false;
-  static const int lib_min_m = env_int("FI_INT4_LIBRARY_MIN_M", 129);
-  if (lib_min_m > 0 && M >= lib_min_m) {
+  if (M >= kLibraryMinM) {
     pl.library = true;
     pl.mt = 0;
     pl.splits = 1;
     return pl;
   }
-  if (M <= gemv_limit() && (M + 15) / 16 <= 65535) {
+  if (M <= kGemvMaxM && (M + 15) / 16 <= 65535) {
     pl.gemv_rows = 16;
     pl.mt = 16;
     pl.splits = 1;
@@ -713,8 +704,6 @@ inline Plan plan(int64_t M, int64_t N, int64_t K) {
     const int64_t cap = std::max<int64_t>(1, K / (16 * std::max<int64_t>(M, 1)));
     s = std::min<int64_t>(std::min<int64_t>(s, cap), groups);
   }
-  static const int forced = env_int("FI_INT4_SPLITS", 0);
-  if (forced > 0) s = std::min<int64_t>(forced, groups);
   // every split gets the same whole number of groups
   const int64_t per = (groups + s - 1) / std::max<int64_t>(s, 1);
   pl.splits = (int)((groups + per - 1) / std::max<int64_t>(per, 1));
@@ -774,12 +763,10 @@ int check_linear(const char* fn, const void* x, int64_t x_stride, int64_t M, int
 }
 
 // Packed weights at 17..64 rows go through gemm_dma_kernel when its scale table holds a
-// split's groups and its 32-bit copy offsets cover the operands.  FI_INT4_DMA=0 keeps
-// gemm_kernel (tuning).
+// split's groups and its 32-bit copy offsets cover the operands.
 bool dma_ok(const fi::gemm::Params& p, const fi::gemm::Plan& pl) {
   using namespace fi::gemm;
-  static const int env = env_int("FI_INT4_DMA", 1);
-  if (!env || (pl.mt != 32 && pl.mt != 64) || p.groups_per_split > kDmaMaxGroups) return false;
+  if ((pl.mt != 32 && pl.mt != 64) || p.groups_per_split > kDmaMaxGroups) return false;
   const int64_t x_span = (int64_t)pl.mt * p.x_stride * 2 + (int64_t)p.K * 2;
   const int64_t w_span = (int64_t)kNTile * p.w_stride + p.K / 2;
   return x_span < (1ll << 31) - 4096 && w_span < (1ll << 31) - 4096;
@@ -866,9 +853,10 @@ size_t split_bytes(int64_t M, int64_t N, const fi::gemm::Plan& pl) {
 // into LDS once); otherwise a separate RMSNorm pass writes the normalized rows into the
 // workspace first (every column tile would re-read and re-normalize its rows).
 bool fuse_norm(int64_t M, int64_t K, const fi::gemm::Plan& pl) {
-  static const int max_m = fi::gemm::env_int("FI_RMSNORM_FUSE_MAX_M", 4);
-  // the decode kernel keeps its normalized rows in LDS: at most 64 KB of them
-  return pl.gemv_rows && M <= max_m && std::min<int64_t>(M, 16) * K * 2 <= 65536;
+  // up to 4 rows (measured: the fused call is faster than norm pass + GEMM there); the
+  // decode kernel keeps its normalized rows in LDS: at most 64 KB of them
+  constexpr int64_t kFuseMaxM = 4;
+  return pl.gemv_rows && M <= kFuseMaxM && std::min<int64_t>(M, 16) * K * 2 <= 65536;
 }
 
 size_t round256(int64_t n) { return (size_t)((n + 255) / 256 * 256); }

@@ -143,14 +143,15 @@ __device__ __forceinline__ void consume_tile(const Params& p, const char* buf, b
   const float m_new = fmaxf(m_run, tmax);
   const float alpha = fast_exp2(m_run - m_new);
   m_run = m_new;
+  // P is rounded to fp16 for the PV MFMA; l sums those same rounded values, so the
+  // numerator and the denominator use identical weights.
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
   half4 pf;
-  float psum = 0.f;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const float e = fast_exp2(x[r] - m_new);
-    psum += e;
-    pf[r] = (half_t)e;
-  }
+  for (int r = 0; r < 4; ++r) pf[r] = (half_t)fast_exp2(x[r] - m_new);
+  const h2 one2 = {(half_t)1.f, (half_t)1.f};
+  float psum = __builtin_amdgcn_fdot2(h2{pf[0], pf[1]}, one2, 0.f, false);
+  psum = __builtin_amdgcn_fdot2(h2{pf[2], pf[3]}, one2, psum, false);
   l_run = l_run * alpha + psum;
 
   // O^T += V^T * P^T (16 keys): lane (col, g) of the transpose read gets keys 4g..4g+3
@@ -362,25 +363,10 @@ __global__ __launch_bounds__(kHeadDim) void merge_kernel(Params p) {
 // partitions keep every CU streaming at small batch; longer ones amortise the
 // workgroup's table and merge work; the merge reads ~0.5 KiB per partition and head).
 // A context of at most 512 tokens is one partition with no merge.
-// FI_DECODE_TOKENS_PER_SPLIT / FI_DECODE_TARGET_WGS override (tuning sweeps).
 static int tokens_per_split(int64_t batch, int64_t wg_per_row, int64_t num_tokens) {
-  static int env_tps = -1;
-  if (env_tps < 0) {
-    const char* s = getenv("FI_DECODE_TOKENS_PER_SPLIT");
-    env_tps = s ? atoi(s) : 0;
-    if (env_tps < 0) env_tps = 0;
-  }
-  static int env_target = -1;
-  if (env_target < 0) {
-    const char* s = getenv("FI_DECODE_TARGET_WGS");
-    env_target = s ? atoi(s) : 0;
-    if (env_target < 0) env_target = 0;
-  }
-  const int64_t target = env_target > 0 ? env_target : 2048;
+  constexpr int64_t target = 2048;
   int64_t tps;
-  if (env_tps > 0) {
-    tps = env_tps;
-  } else if (num_tokens <= 512) {
+  if (num_tokens <= 512) {
     tps = num_tokens;
   } else {
     const int64_t per_row = batch * wg_per_row;
@@ -421,49 +407,50 @@ extern "C" size_t fi_paged_attention_workspace_size(int64_t batch, int64_t num_q
   return (size_t)(batch * num_q_heads * splits * (fi::kHeadDim + 2) * sizeof(float));
 }
 
-extern "C" int fi_paged_attention_fwd(const void* q, int64_t q_sb, int64_t q_sh,
-                                      const void* k_cache, const void* v_cache,
-                                      int64_t num_pool_blocks, int64_t block_size,
-                                      int64_t num_kv_heads, const int32_t* block_table,
-                                      int64_t bt_stride, int64_t max_blocks_per_seq,
-                                      const int32_t* context_lens, int64_t num_tokens, void* o,
-                                      int64_t o_sb, int64_t o_sh, int64_t batch,
-                                      int64_t num_q_heads, int64_t head_dim, float sm_scale,
-                                      void* workspace, size_t workspace_bytes, void* stream) {
+namespace {
+
+// Validation and launch shared by both entry points.  `fn` names the entry point in
+// error messages; `workspace` is the caller's buffer or the library's static scratch.
+int paged_fwd(const char* fn, const void* q, int64_t q_sb, int64_t q_sh, const void* k_cache,
+              const void* v_cache, int64_t num_pool_blocks, int64_t block_size,
+              int64_t num_kv_heads, const int32_t* block_table, int64_t bt_stride,
+              int64_t max_blocks_per_seq, const int32_t* context_lens, int64_t num_tokens,
+              void* o, int64_t o_sb, int64_t o_sh, int64_t batch, int64_t num_q_heads,
+              int64_t head_dim, float sm_scale, void* workspace, size_t workspace_bytes,
+              void* stream) {
   using namespace fi;
   using namespace fi::decode;
-  clear_error();
   if (head_dim != kHeadDim) {
-    set_error("fi_paged_attention_fwd: head_dim %lld not supported (only %d)",
+    set_error("%s: head_dim %lld not supported (only %d)", fn,
               (long long)head_dim, kHeadDim);
     return FI_ERR_UNSUPPORTED;
   }
   if (batch < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || num_tokens < 0 ||
       num_pool_blocks < 0 || max_blocks_per_seq < 0 || num_q_heads % num_kv_heads != 0) {
-    set_error("fi_paged_attention_fwd: invalid sizes (batch %lld, heads %lld/%lld, tokens %lld)",
+    set_error("%s: invalid sizes (batch %lld, heads %lld/%lld, tokens %lld)", fn,
               (long long)batch, (long long)num_q_heads, (long long)num_kv_heads,
               (long long)num_tokens);
     return FI_ERR_INVALID;
   }
   if (block_size <= 0 || block_size % 16 != 0) {
-    set_error("fi_paged_attention_fwd: block_size %lld must be a positive multiple of 16",
+    set_error("%s: block_size %lld must be a positive multiple of 16", fn,
               (long long)block_size);
     return FI_ERR_UNSUPPORTED;
   }
   if (batch == 0) return FI_OK;
   if (num_tokens > (int64_t)kMaxSplitTokens * kMaxSplits ||
       block_size * num_kv_heads * kHeadDim * 2 > ((int64_t)1 << 30)) {
-    set_error("fi_paged_attention_fwd: num_tokens %lld or block bytes too large",
+    set_error("%s: num_tokens %lld or block bytes too large", fn,
               (long long)num_tokens);
     return FI_ERR_UNSUPPORTED;
   }
   if (!q || !k_cache || !v_cache || !o || (!block_table && num_tokens > 0)) {
-    set_error("fi_paged_attention_fwd: null pointer");
+    set_error("%s: null pointer", fn);
     return FI_ERR_INVALID;
   }
   if (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) & 15u ||
       (q_sb | q_sh) % 8 != 0) {
-    set_error("fi_paged_attention_fwd: q and the pools must be 16-byte aligned");
+    set_error("%s: q and the pools must be 16-byte aligned", fn);
     return FI_ERR_INVALID;
   }
 
@@ -501,7 +488,7 @@ extern "C" int fi_paged_attention_fwd(const void* q, int64_t q_sb, int64_t q_sh,
     const size_t need =
         fi_paged_attention_workspace_size(batch, num_q_heads, num_kv_heads, num_tokens, head_dim);
     if (!workspace || workspace_bytes < need) {
-      set_error("fi_paged_attention_fwd: workspace of %zu bytes needed, %zu given", need,
+      set_error("%s: workspace of %zu bytes needed, %zu given", fn, need,
                 workspace ? workspace_bytes : (size_t)0);
       return FI_ERR_WORKSPACE;
     }
@@ -509,14 +496,32 @@ extern "C" int fi_paged_attention_fwd(const void* q, int64_t q_sb, int64_t q_sh,
     p.part_ml = p.part_o + batch * num_q_heads * splits * kHeadDim;
   }
   if (batch > 65535 || splits > 65535) {
-    set_error("fi_paged_attention_fwd: grid too large");
+    set_error("%s: grid too large", fn);
     return FI_ERR_UNSUPPORTED;
   }
   const dim3 grid((unsigned)wg_per_row, (unsigned)splits, (unsigned)batch);
   hipLaunchKernelGGL(partition_kernel, grid, dim3(kWaves * 64), 0, (hipStream_t)stream, p);
-  int rc = check_launch("fi_paged_attention_fwd(partition)");
+  int rc = check_launch(fn);
   if (rc != FI_OK || p.direct) return rc;
   hipLaunchKernelGGL(merge_kernel, dim3((unsigned)num_q_heads, (unsigned)batch), dim3(kHeadDim), 0,
                      (hipStream_t)stream, p);
-  return check_launch("fi_paged_attention_fwd(merge)");
+  return check_launch(fn);
+}
+
+}  // namespace
+
+extern "C" int fi_paged_attention_fwd(const void* q, int64_t q_sb, int64_t q_sh,
+                                      const void* k_cache, const void* v_cache,
+                                      int64_t num_pool_blocks, int64_t block_size,
+                                      int64_t num_kv_heads, const int32_t* block_table,
+                                      int64_t bt_stride, int64_t max_blocks_per_seq,
+                                      const int32_t* context_lens, int64_t num_tokens, void* o,
+                                      int64_t o_sb, int64_t o_sh, int64_t batch,
+                                      int64_t num_q_heads, int64_t head_dim, float sm_scale,
+                                      void* workspace, size_t workspace_bytes, void* stream) {
+  fi::clear_error();
+  return paged_fwd("fi_paged_attention_fwd", q, q_sb, q_sh, k_cache, v_cache, num_pool_blocks,
+                   block_size, num_kv_heads, block_table, bt_stride, max_blocks_per_seq,
+                   context_lens, num_tokens, o, o_sb, o_sh, batch, num_q_heads, head_dim,
+                   sm_scale, workspace, workspace_bytes, stream);
 }

@@ -18,10 +18,13 @@ Differences, all keyword-only or internal:
   always has ``ceil(max_seq_len / block_size)`` blocks, shared by every row); rows
   then hold ``ceil(max_seq_len / block_size)`` entries.  Without it the reference
   sizes are used (rows as wide as the pool, :21-22).
-* The allocator works on a host copy of the table, so allocation never waits for
-  the device (the reference's ``.item()`` at :60); the device tensor returned by
-  ``block_table`` is refreshed from it before use.  Assigning ``block_table`` replaces
-  both copies.  Mutate the table through ``alloc_block`` or assignment.
+* The allocator decides on a host copy of the table, so allocation never waits for
+  the device (the reference's ``.item()`` at :60).  ``block_table`` is a device tensor
+  like the reference's; the entries ``alloc_block`` fills are written into it (batched,
+  before the tensor is next handed out), never the whole table, so a caller's in-place
+  writes to other entries persist.  Such writes are not seen by the allocator, which
+  still picks the first entry it has not filled itself; assigning ``block_table``
+  replaces both copies.
 * ``store``/``store_batch`` (:69-103) copy with the HIP scatter kernel.  A position
   whose table entry is -1 is skipped (the reference's ``k[layer, -1, ...]`` would wrap
   to the last pool block).
@@ -64,22 +67,26 @@ class KVCache:
         self._table = np.full((1, self.max_blocks_per_seq), -1, dtype=np.int32)
         self._table_dev = torch.full((1, self.max_blocks_per_seq), -1, dtype=torch.int32,
                                      device=self.device)
-        self._dirty = False
+        self._pending: list[tuple[int, int, int]] = []  # (row, entry, block) not yet on device
 
         self.free_blocks = list(range(self.num_blocks))
         self._allocated = 0
         self.num_tokens = 0
 
     # -- block table ---------------------------------------------------------------
+    def _flush(self) -> None:
+        """Write the entries alloc_block filled since the last flush into the device table."""
+        if self._pending:
+            rows, cols, vals = zip(*self._pending)
+            self._pending = []
+            idx = torch.tensor([rows, cols], dtype=torch.int64).to(self.device)
+            self._table_dev.index_put_((idx[0], idx[1]),
+                                       torch.tensor(vals, dtype=torch.int32).to(self.device))
+
     @property
     def block_table(self) -> torch.Tensor:
         """Device block table [batch, max_blocks_per_seq] (int32, -1 = unallocated)."""
-        if self._dirty:
-            if tuple(self._table_dev.shape) != self._table.shape:
-                self._table_dev = torch.from_numpy(self._table.copy()).to(self.device)
-            else:
-                self._table_dev.copy_(torch.from_numpy(self._table))
-            self._dirty = False
+        self._flush()
         return self._table_dev
 
     @block_table.setter
@@ -89,25 +96,31 @@ class KVCache:
             raise ValueError("block_table must be 2-D")
         self._table = table.detach().to("cpu", torch.int32).numpy().copy()
         self._table_dev = table.detach().to(self.device, torch.int32).contiguous()
-        self._dirty = False
+        self._pending = []
 
     def host_block_table(self) -> np.ndarray:
-        """Read-only view of the host copy of the table (no device traffic)."""
+        """Read-only view of the allocator's host copy of the table (no device traffic)."""
         v = self._table.view()
         v.flags.writeable = False
         return v
 
     def _grow_batch(self, batch_size: int):
-        """Expand block_table for larger batch (new rows are -1)."""
-        if batch_size <= self._table.shape[0]:
+        """Add rows of -1 entries until the table has batch_size rows (kv_cache.py:41-48)."""
+        rows = self._table.shape[0]
+        if batch_size <= rows:
             return
         new_table = np.full((batch_size, self.max_blocks_per_seq), -1, dtype=np.int32)
-        new_table[:self._table.shape[0]] = self._table
+        new_table[:rows] = self._table
         self._table = new_table
-        self._dirty = True
+        self._flush()
+        new_dev = torch.full((batch_size, self.max_blocks_per_seq), -1, dtype=torch.int32,
+                             device=self.device)
+        new_dev[:rows] = self._table_dev
+        self._table_dev = new_dev
 
     def alloc_block(self, batch_idx: int = 0) -> int:
-        """Allocate a new block for a sequence. Returns logical block index."""
+        """Take the lowest free physical block id, put it in the first unallocated entry of
+        row ``batch_idx`` and return that entry's index (kv_cache.py:50-63)."""
         if not self.free_blocks:
             raise RuntimeError("KV cache out of memory")
         phys_block = self.free_blocks.pop(0)
@@ -118,7 +131,7 @@ class KVCache:
         logical_idx = int(empty_slots[0])
         row[logical_idx] = phys_block
         self._allocated += 1
-        self._dirty = True
+        self._pending.append((int(batch_idx), logical_idx, int(phys_block)))
         return logical_idx
 
     def allocated_blocks(self, batch_idx: int = 0) -> int:
@@ -126,7 +139,7 @@ class KVCache:
         return int(np.count_nonzero(self._table[batch_idx] >= 0))
 
     def get_physical_blocks(self, batch_idx: int = 0) -> torch.Tensor:
-        """Return tensor of physical block indices for a sequence."""
+        """Row ``batch_idx`` of the device table (kv_cache.py:65-67)."""
         return self.block_table[batch_idx]
 
     # -- stores ----------------------------------------------------------------------
@@ -150,9 +163,11 @@ class KVCache:
         return self._allocated * self.block_size
 
     def reset(self):
-        """Free all blocks (for a new sequence)."""
+        """Every entry back to -1, every block back on the free list, token count 0
+        (kv_cache.py:108-113)."""
         self._table.fill(-1)
-        self._dirty = True
+        self._pending = []
+        self._table_dev.fill_(-1)
         self.free_blocks = list(range(self.num_blocks))
         self._allocated = 0
         self.num_tokens = 0

@@ -4,7 +4,7 @@
 (kernels/matmul.py:217-231): ``w`` is either a ``(packed_int8, scales)`` tuple — the
 dequantization then runs inside the MFMA loop — or an fp16 ``[N, K]`` weight.
 ``quantize_int4_groupwise`` (loader.py:9-41) and ``dequantize_int4`` (the reference's
-``_dequant_storage``, matmul.py:197-214) produce and expand the same wire format, bit for
+``_dequant_storage``, matmul.py:309-326) produce and expand the same wire format, bit for
 bit.  ``rms_norm`` is kernels/rms_norm.py's; ``rms_norm_int4_matmul`` is the norm of
 model.py:82 and the projection after it in one call.
 """
@@ -32,14 +32,20 @@ def _rows16(t: torch.Tensor, elem: int) -> torch.Tensor:
 
 
 # Split-K calls need a workspace for their fp32 partials; one per (device, stream), grown
-# on demand, so back-to-back calls on a stream reuse it.
+# on demand, so back-to-back calls on a stream reuse it.  A buffer that is outgrown is
+# kept alive, never returned to the allocator: a HIP graph captured earlier may hold its
+# address (graphs captured on one stream share the key), and replaying that graph must
+# not write into memory that was handed out again.
 _workspaces: dict[tuple[int, int], torch.Tensor] = {}
+_outgrown: list[torch.Tensor] = []
 
 
 def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
     key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
+        if ws is not None:
+            _outgrown.append(ws)
         ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _workspaces[key] = ws
     return ws
@@ -184,7 +190,7 @@ def quantize_int4_groupwise(w: torch.Tensor, groupsize: int = 128
 
 def dequantize_int4(packed: torch.Tensor, scales: torch.Tensor,
                     groupsize: int = 128) -> torch.Tensor:
-    """kernels/matmul.py:197-214 (``_dequant_storage``): -> fp16 ``[N, K]``, each weight
+    """kernels/matmul.py:309-326 (``_dequant_storage``): -> fp16 ``[N, K]``, each weight
     fp16(q * scale)."""
     _need_cuda("packed", packed)
     N, K = packed.shape[0], packed.shape[1] * 2

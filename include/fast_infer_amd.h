@@ -1,8 +1,8 @@
 /*
  * fast_infer_amd — C ABI of the MI355X (gfx950) attention hot path.
  *
- * Three device operations, each a drop-in for one piece of Fast_Infer's
- * attention path:
+ * Entry points, each a drop-in for one piece of Fast_Infer's attention path or of
+ * the operations on either side of it:
  *
  *   fi_flash_attention_fwd   causal prefill attention
  *                            replaces kernels/attention.py:80-113 (flash_attention,
@@ -16,6 +16,15 @@
  *                            replaces model.py:162-183 (_store_kv_prefill copies),
  *                            model.py:185-201 (_store_kv_decode copies) and
  *                            kv_cache.py:69-103 (KVCache.store / store_batch).
+ *   fi_rope_store_kv         RoPE on q/k (kernels/rope.py:26-44 at model.py:101), with
+ *                            the K/V pool write that follows it in the same pass.
+ *   fi_kv_append / fi_kv_release / fi_kv_reset
+ *                            the block allocator of kv_cache.py:50-63 / :108-113 as
+ *                            model.py drives it, with per-row lengths, on the device.
+ *   fi_int4_matmul, fi_int4_quantize, fi_int4_dequantize, fi_rmsnorm,
+ *   fi_rmsnorm_int4_matmul   the INT4 projections and RMSNorm around attention
+ *                            (kernels/matmul.py:217-231, loader.py:9-41,
+ *                            kernels/matmul.py:309-326, kernels/rms_norm.py:29-43).
  *
  * Conventions shared by every entry point:
  *   - Pointers are device pointers; sizes and strides are int64 and counted in
@@ -27,7 +36,10 @@
  *     [0, num_blocks) are never dereferenced: rows that map there are skipped.
  *   - `stream` is a hipStream_t (NULL = the legacy default stream).  Every call
  *     is asynchronous: it enqueues work and returns; nothing synchronises.
- *   - The library keeps no mutable global state; calls are reentrant.
+ *   - Calls are reentrant.  The library's only host-side state is the per-thread
+ *     error message and, for prefill-sized fi_int4_matmul calls (M >= 129), one
+ *     rocBLAS handle per device, created on first use under a mutex and kept until
+ *     the process ends.
  *   - Return value: FI_OK or an FI_ERR_* code; fi_last_error() then gives a
  *     message for the calling thread.
  *   - Only head_dim == 128 and fp16 data are implemented (the shapes of
@@ -310,7 +322,7 @@ FI_API int fi_int4_quantize(const void* w, int64_t w_stride, int64_t N, int64_t 
                      int64_t s_stride, void* stream);
 
 /*
- * _dequant_storage (kernels/matmul.py:197-214): w[n, k] = fp16(q[n, k] * scale[n, k/128]).
+ * _dequant_storage (kernels/matmul.py:309-326): w[n, k] = fp16(q[n, k] * scale[n, k/128]).
  */
 FI_API int fi_int4_dequantize(const void* packed, int64_t p_stride, const void* scales,
                        int64_t s_stride, int64_t N, int64_t K, int64_t groupsize, void* w,

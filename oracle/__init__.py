@@ -18,7 +18,7 @@ Contents (each function cites the reference file:line it restates):
 * ``block_manager`` — the reference allocator driven with per-row token counts, plus
   row release (the device block manager's checker).
 * ``int4`` — numpy restatement of the INT4 weight format: quantize (loader.py:9-41),
-  unpack / dequantize (matmul.py:197-214), and the float64 product with its error bound.
+  unpack / dequantize (matmul.py:309-326), and the float64 product with its error bound.
 * ``rmsnorm`` — RMSNorm (kernels/rms_norm.py:8-43) in float64 and its fp16 error bound.
 * ``ref_algo.c`` (+ ``native``) — the same tile algorithms in C with OpenMP, used
   as the CPU baseline ("port").

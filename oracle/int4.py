@@ -8,7 +8,7 @@
   reciprocal of the scalar (ATen's BinaryDivTrueKernel.cu), then rounded to fp16;
   ``round(w / scale)`` — an fp32 quotient rounded to fp16, then rounded half to even;
   clamp to [-8, 7]; packing (:31-36) puts k = 2j in the low nibble of byte j.
-* ``unpack`` / ``dequantize`` — matmul.py:197-214 (``_dequant_storage``): nibble >= 8 means
+* ``unpack`` / ``dequantize`` — matmul.py:309-326 (``_dequant_storage``): nibble >= 8 means
   nibble - 16; weight = fp16(fp32(q) * fp32(scale)).
 * ``matmul_exact`` — sum_k x[m, k] * w[n, k] in float64, the value an fp32-accumulating
   kernel approximates (matmul.py:14-132 fused; :135-186 on dequantized weights).
@@ -51,7 +51,7 @@ def quantize_int4_groupwise(w: np.ndarray, groupsize: int = GROUP, true_division
 
 
 def unpack(packed: np.ndarray) -> np.ndarray:
-    """int8 [N, K/2] -> int8 [N, K] in [-8, 7] (matmul.py:202-207)."""
+    """int8 [N, K/2] -> int8 [N, K] in [-8, 7] (matmul.py:316-321)."""
     b = packed.view(np.uint8).astype(np.int16)
     low = b & 0xF
     high = (b >> 4) & 0xF
@@ -61,7 +61,7 @@ def unpack(packed: np.ndarray) -> np.ndarray:
 
 
 def dequantize(packed: np.ndarray, scales: np.ndarray, groupsize: int = GROUP) -> np.ndarray:
-    """matmul.py:197-214 -> fp16 [N, K]."""
+    """matmul.py:309-326 -> fp16 [N, K]."""
     q = unpack(packed).astype(np.float32)
     N, K = q.shape
     s = np.repeat(scales.astype(np.float32), groupsize, axis=1)

@@ -113,6 +113,34 @@ def test_decode_step_graph_replay(hip, B):
         assert torch.isfinite(noise)
 
 
+def test_int4_workspace_two_captures_shared_pool(hip):
+    """Two graphs captured back to back on a shared memory pool, the second needing a larger
+    split-K workspace than the first: the first graph's workspace must stay allocated, so
+    replaying both (in either order, repeatedly) equals the eager results bit for bit."""
+    banner("int4 split-K workspace across two captures (17 then 64 rows)")
+    from fast_infer_amd import int4_matmul, quantize_int4_groupwise
+
+    g = torch.Generator(device=DEV).manual_seed(77)
+    w = quantize_int4_groupwise((torch.randn(5120, 3072, device=DEV, generator=g) * 0.02).half())
+    xs = {m: torch.randn(m, 3072, device=DEV, generator=g).half() for m in (17, 64)}
+    refs = {m: int4_matmul(x, w).clone() for m, x in xs.items()}
+    torch.cuda.synchronize()
+    pool = torch.cuda.graph_pool_handle()
+    graphs, outs = {}, {}
+    for m in (17, 64):
+        graphs[m] = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graphs[m], pool=pool):
+            outs[m] = int4_matmul(xs[m], w)
+        torch.cuda.synchronize()
+    for rep in range(3):
+        for m in ((17, 64) if rep % 2 == 0 else (64, 17)):
+            outs[m].zero_()
+            graphs[m].replay()
+        torch.cuda.synchronize()
+        for m in (17, 64):
+            assert torch.equal(outs[m], refs[m]), (rep, m)
+
+
 def test_block_manager_append_graph_replay(hip):
     banner("graph capture of PagedKVCache.append")
     from fast_infer_amd import PagedKVCache

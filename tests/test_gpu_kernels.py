@@ -431,3 +431,54 @@ def test_flash_prefill_batch4_seq4096_sampled(hip):
     ref = OA.causal_attention_rows(q.cpu(), k.cpu(), v.cpu(), rows, heads)
     got = out.cpu()[:, heads][:, :, rows]
     assert _maxabs(got, ref) <= ATOL
+
+
+@pytest.mark.parametrize("S", [1, 70, 200])
+def test_zero_scale_prefill_and_decode(hip, S):
+    """sm_scale == 0: uniform weights over the causal prefix (prefill) or the context
+    (decode); masked keys must not turn into NaN."""
+    banner(f"zero sm_scale prefill and decode, S={S}")
+    from fast_infer_amd import flash_attention, paged_attention
+
+    B, H, Hkv = 2, 24, 8
+    g = torch.Generator().manual_seed(60 + S)
+    q = torch.randn(B, S, H, 128, generator=g).half().transpose(1, 2)
+    k = torch.randn(B, S, Hkv, 128, generator=g).half().transpose(1, 2)
+    v = torch.randn(B, S, Hkv, 128, generator=g).half().transpose(1, 2)
+    out = flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), 0.0)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out).all())
+    assert _maxabs(out, OA.causal_attention(q, k, v, 0.0)) <= ATOL
+    nb = math.ceil(S / 64)
+    kc = torch.randn(B * nb + 1, 64, Hkv, 128, generator=g).half()
+    vc = torch.randn(B * nb + 1, 64, Hkv, 128, generator=g).half()
+    table = torch.arange(B * nb, dtype=torch.int32).view(B, nb).flip(0).contiguous()
+    qd = torch.randn(B, H, 128, generator=g).half()
+    od = paged_attention(qd.to(DEV), kc.to(DEV), vc.to(DEV), table.to(DEV), 64, S, 0.0)
+    torch.cuda.synchronize()
+    assert _maxabs(od, OA.paged_attention(qd, kc, vc, table, 64, S, sm_scale=0.0)) <= ATOL
+
+
+def test_kvcache_device_table_keeps_in_place_writes(hip):
+    """block_table is a device tensor updated in place: alloc_block writes only the
+    entries it fills, so a caller's own writes to other entries persist."""
+    banner("KVCache device table in-place writes")
+    from fast_infer_amd import KVCache
+
+    cache = KVCache(1, 8, 128, max_seq_len=512, block_size=64, device=DEV, num_blocks=20)
+    cache._grow_batch(2)
+    cache.alloc_block(0)
+    table = cache.block_table
+    table[1, 5] = 17            # the caller's own entry
+    cache.alloc_block(0)
+    cache.alloc_block(1)
+    cache._grow_batch(3)
+    cache.alloc_block(2)
+    got = cache.block_table.cpu()
+    expect = torch.full((3, 8), -1, dtype=torch.int32)
+    expect[0, 0], expect[0, 1], expect[1, 0], expect[2, 0] = 0, 1, 2, 3
+    expect[1, 5] = 17
+    assert torch.equal(got, expect)
+    assert cache.host_block_table()[1, 5] == -1   # not seen by the allocator
+    cache.reset()
+    assert bool((cache.block_table == -1).all())

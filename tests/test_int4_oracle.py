@@ -2,7 +2,7 @@
 
 The reference ships no INT4 vectors; the oracle is pinned by hand-packed bytes, by the
 closed-form properties of symmetric rounding quantization, and by torch's own CPU
-arithmetic running the reference's expressions (loader.py:20-38, matmul.py:197-214) —
+arithmetic running the reference's expressions (loader.py:20-38, matmul.py:309-326) —
 torch as an independent fp16/fp32 arithmetic engine, not the reference's code.
 """
 

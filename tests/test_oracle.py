@@ -148,6 +148,24 @@ def test_causal_equal_keys_give_running_mean_of_v():
     assert torch.allclose(o, mean.expand(1, 2, S, 128), atol=1e-12)
 
 
+def test_zero_scale_gives_running_mean_of_v():
+    # sm_scale == 0: every score is 0, so each row averages V over its causal prefix; the
+    # decode oracle averages V over the context
+    g = torch.Generator().manual_seed(16)
+    S = 70
+    q = torch.randn(1, 6, S, 128, generator=g)
+    k = torch.randn(1, 2, S, 128, generator=g)
+    v = torch.randn(1, 2, S, 128, generator=g)
+    o = OA.causal_attention(q, k, v, 0.0, dtype=torch.float64)
+    mean = torch.cumsum(v.double(), dim=2) / torch.arange(1, S + 1, dtype=torch.float64)[:, None]
+    assert torch.allclose(o, mean.repeat_interleave(3, dim=1), atol=1e-12)
+    sp = dict(specs.DECODE_CASES["decode_ctx200"])
+    qd, kc, vc, table, lens = specs.decode_inputs(sp)
+    od = OA.paged_attention(qd, kc, vc, table, sp["bs"], lens, sm_scale=0.0, dtype=torch.float64)
+    _, V = OA.gather_context(kc.double(), vc.double(), table.numpy(), sp["bs"], 0, lens[0])
+    assert torch.allclose(od[0], V.mean(0).repeat_interleave(3, dim=0), atol=1e-12)
+
+
 def test_one_hot_v_reads_softmax_weights():
     g = torch.Generator().manual_seed(7)
     S = 20
