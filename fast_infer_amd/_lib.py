@@ -60,6 +60,17 @@ SIGNATURES = {
          _ptr, _sz,                              # workspace
          _ptr],                                  # stream
     ),
+    "fi_paged_attention_fwd_noalloc": (
+        ctypes.c_int,
+        [_ptr, _i64, _i64,                       # q, strides
+         _ptr, _ptr, _i64, _i64, _i64,           # pools, N, block_size, Hkv
+         _ptr, _i64, _i64,                       # block table, stride, max blocks
+         _ptr, _i64,                             # context_lens, num_tokens
+         _ptr, _i64, _i64,                       # o, strides
+         _i64, _i64, _i64,                       # batch Hq D
+         _f32,                                   # sm_scale
+         _ptr],                                  # stream
+    ),
     "fi_kv_store": (
         ctypes.c_int,
         [_ptr, _i64, _i64, _i64,

@@ -17,6 +17,8 @@
 //     O^T = V^T * P^T (v_mfma_f32_16x16x16_f16, V^T fragments from the LDS transpose
 //     read ds_read_b64_tr_b16, P^T straight from the S^T accumulator lanes).
 //   * Online softmax is fp32 in log2 units (exp2 with sm_scale * log2(e) folded in).
+#include <mutex>
+
 #include "common.h"
 
 namespace fi {
@@ -508,6 +510,40 @@ int paged_fwd(const char* fn, const void* q, int64_t q_sb, int64_t q_sh, const v
   return check_launch(fn);
 }
 
+// Scratch of fi_paged_attention_fwd_noalloc: the split-K partials, in a file-scope device
+// array.  Each device holds its own copy from module load until the process ends.  Host
+// code never uses the array's name as an address (on the host it is only a stand-in for
+// the symbol): the device address comes from hipGetSymbolAddress, once per device.
+constexpr size_t kScratchBytes = FI_PAGED_NOALLOC_SCRATCH_BYTES;
+__device__ __attribute__((aligned(256))) char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The scratch address on the current device (looked up on the first call there).
+int scratch_address(const char* fn, void** out) {
+  using namespace fi;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("%s: no usable current HIP device", fn);
+    return FI_ERR_HIP;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      set_error("%s: hipGetSymbolAddress(scratch) failed on device %d: %s", fn, dev,
+                hipGetErrorString(e));
+      return FI_ERR_HIP;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return FI_OK;
+}
+
 }  // namespace
 
 extern "C" int fi_paged_attention_fwd(const void* q, int64_t q_sb, int64_t q_sh,
@@ -524,4 +560,37 @@ extern "C" int fi_paged_attention_fwd(const void* q, int64_t q_sb, int64_t q_sh,
                    block_size, num_kv_heads, block_table, bt_stride, max_blocks_per_seq,
                    context_lens, num_tokens, o, o_sb, o_sh, batch, num_q_heads, head_dim,
                    sm_scale, workspace, workspace_bytes, stream);
+}
+
+extern "C" int fi_paged_attention_fwd_noalloc(const void* q, int64_t q_sb, int64_t q_sh,
+                                              const void* k_cache, const void* v_cache,
+                                              int64_t num_pool_blocks, int64_t block_size,
+                                              int64_t num_kv_heads, const int32_t* block_table,
+                                              int64_t bt_stride, int64_t max_blocks_per_seq,
+                                              const int32_t* context_lens, int64_t num_tokens,
+                                              void* o, int64_t o_sb, int64_t o_sh,
+                                              int64_t batch, int64_t num_q_heads,
+                                              int64_t head_dim, float sm_scale, void* stream) {
+  using namespace fi;
+  static const char* fn = "fi_paged_attention_fwd_noalloc";
+  clear_error();
+  const size_t need = batch > 0 && num_tokens > 0
+                          ? fi_paged_attention_workspace_size(batch, num_q_heads, num_kv_heads,
+                                                              num_tokens, head_dim)
+                          : 0;
+  if (need > kScratchBytes) {
+    set_error("%s: these sizes need %zu bytes of split-K scratch, more than the %zu bytes "
+              "this entry point holds per device; use fi_paged_attention_fwd with a workspace",
+              fn, need, kScratchBytes);
+    return FI_ERR_UNSUPPORTED;
+  }
+  void* ws = nullptr;
+  if (need) {
+    const int rc = scratch_address(fn, &ws);
+    if (rc != FI_OK) return rc;
+  }
+  return paged_fwd(fn, q, q_sb, q_sh, k_cache, v_cache, num_pool_blocks, block_size,
+                   num_kv_heads, block_table, bt_stride, max_blocks_per_seq, context_lens,
+                   num_tokens, o, o_sb, o_sh, batch, num_q_heads, head_dim, sm_scale, ws,
+                   need ? kScratchBytes : 0, stream);
 }

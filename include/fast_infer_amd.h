@@ -144,6 +144,29 @@ FI_API int fi_paged_attention_fwd(const void* q, int64_t q_sb, int64_t q_sh,
                            void* stream);
 
 /*
+ * fi_paged_attention_fwd without a workspace argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  Same arguments, results and errors as
+ * fi_paged_attention_fwd; the split-K partials go to a static per-device scratch array of
+ * FI_PAGED_NOALLOC_SCRATCH_BYTES bytes inside the library (each GPU the library runs on
+ * holds it until the process ends).  Sizes whose
+ * fi_paged_attention_workspace_size exceeds that return FI_ERR_UNSUPPORTED.  The call
+ * allocates nothing.  Every call on one GPU shares that GPU's scratch: calls that overlap
+ * in time on one GPU (concurrent streams, or host threads) race and must not be issued.
+ * The stream must belong to the current HIP device.
+ */
+#define FI_PAGED_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+FI_API int fi_paged_attention_fwd_noalloc(const void* q, int64_t q_sb, int64_t q_sh,
+                                   const void* k_cache, const void* v_cache,
+                                   int64_t num_pool_blocks, int64_t block_size,
+                                   int64_t num_kv_heads, const int32_t* block_table,
+                                   int64_t bt_stride, int64_t max_blocks_per_seq,
+                                   const int32_t* context_lens, int64_t num_tokens, void* o,
+                                   int64_t o_sb, int64_t o_sh, int64_t batch,
+                                   int64_t num_q_heads, int64_t head_dim, float sm_scale,
+                                   void* stream);
+
+/*
  * Scatter K/V rows into the paged pool (byte-exact copies).
  * Replaces the slice copies of model.py:176-183 (prefill), model.py:196-201 (decode)
  * and kv_cache.py:69-103.
