@@ -500,7 +500,7 @@ inline int blas_gemm(const half_t* x, int64_t ldx, const half_t* w, int64_t ldw,
 // so one memory latency covers the chunk; the four waves' sums are added through LDS in
 // a fixed order.
 template <bool kInt4, int kChunk, bool kNorm>
-__global__ __launch_bounds__(kThreads) void gemv_kernel(Params p) {
+__global__ __launch_bounds__(kThreads, kNorm ? 1 : 2) void gemv_kernel(Params p) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int row = lane & 15;
@@ -510,29 +510,30 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(Params p) {
   const int nc = n < p.N ? n : p.N - 1;
   const int m = blockIdx.y * 16 + row;  // the X row this lane supplies
   const bool m_ok = m < p.M;
-  // rows past M load a valid row: MFMA output column j depends on X row j only, and the
-  // columns of rows past M are never stored
+  // MFMA output column j depends on X row j only, and the columns of rows past M are never
+  // stored: those lanes read zeros (or, from the normalized rows in LDS, a valid row)
   const int mc = m_ok ? m : p.M - 1;
   const int groups = p.K / kGroup;
   // fused norm: the workgroup's (at most 16, in practice a few) rows are normalized once
   // into LDS, [rows, K] fp16, and the X operand is read from there
   extern __shared__ __attribute__((aligned(16))) half_t xn[];
   const int rows_n = min(16, p.M - (int)blockIdx.y * 16);
-  if constexpr (kNorm) {
-    for (int r = wave; r < rows_n; r += 4)
-      norm_row_to(p.x + (int64_t)(blockIdx.y * 16 + r) * p.x_stride, p.norm_w, p.K, p.eps,
-                  xn + r * p.K, lane);
-    __syncthreads();
-  }
   const half_t* xrow_n = xn + min(row, rows_n - 1) * p.K;
 
-  floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
-  for (int g0 = wave; g0 < groups; g0 += 4 * kChunk) {
-    // every load of the chunk is issued before any math and without branches (groups past
-    // the end reload the last group and are skipped below), so one latency covers them
-    u32x4 wv[kInt4 ? kChunk : 4 * kChunk];
-    half_t sv[kChunk];
-    u32x4 xv[kNorm ? 1 : 4 * kChunk];
+  // Issue the loads of one chunk (kChunk groups of this wave, g0, g0 + 4, ...): every load
+  // goes out before any math and without branches (groups past the end reload the last
+  // group and are skipped), so one latency covers the chunk.
+  u32x4 wv[kInt4 ? kChunk : 4 * kChunk];
+  half_t sv[kChunk];
+  u32x4 xv[kNorm ? 1 : 4 * kChunk];
+  // X through a buffer descriptor over this workgroup's rows: lanes of rows past M use an
+  // offset past the end and read zeros with no memory request and no branch (the host
+  // checks that the rows span less than 2^31 bytes)
+  const __amdgpu_buffer_rsrc_t xr_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.x + (int64_t)blockIdx.y * 16 * p.x_stride), (short)0,
+      (int)(((int64_t)(rows_n - 1) * p.x_stride + p.K) * 2), 0x00020000);
+  const int x_off0 = m_ok ? (int)(((int64_t)row * p.x_stride + grp * 32) * 2) : 0x7ffffff0;
+  auto load_chunk = [&](int g0) {
 #pragma unroll
     for (int c = 0; c < kChunk; ++c) {
       const int g = min(g0 + 4 * c, groups - 1);
@@ -545,10 +546,34 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(Params p) {
         for (int s = 0; s < 4; ++s) wv[4 * c + s] = *(const u32x4*)(wr + 8 * s);
       }
       if constexpr (!kNorm) {
-        const half_t* xr = p.x + (int64_t)mc * p.x_stride + g * kGroup + grp * 32;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) xv[4 * c + s] = *(const u32x4*)(xr + 8 * s);
+        for (int s = 0; s < 4; ++s)
+          xv[4 * c + s] = __builtin_bit_cast(
+              u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                         xr_rsrc, m_ok ? x_off0 + (g * kGroup + 8 * s) * 2 : x_off0, 0, 0));
       }
+    }
+  };
+
+  // the first chunk's weights are in flight while the rows are normalized; the scheduling
+  // barriers keep every load of a chunk ahead of its math (the scheduler would otherwise
+  // start the math after the first few loads and issue the rest one latency later)
+  load_chunk(wave);
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (kNorm) {
+    for (int r = wave; r < rows_n; r += 4)
+      norm_row_to(p.x + (int64_t)(blockIdx.y * 16 + r) * p.x_stride, p.norm_w, p.K, p.eps,
+                  xn + r * p.K, lane);
+    __syncthreads();
+  }
+
+  // two accumulators, alternating by k-step, halve the chain of dependent MFMAs
+  floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+  floatx4 acc2 = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int g0 = wave; g0 < groups; g0 += 4 * kChunk) {
+    if (g0 != wave) {
+      load_chunk(g0);
+      __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int c = 0; c < kChunk; ++c) {
@@ -565,11 +590,18 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(Params p) {
             xf = *(const u32x4*)(xrow_n + (g0 + 4 * c) * kGroup + grp * 32 + 8 * s);
           else
             xf = xv[4 * c + s];
-          acc = mfma16x16x32(wf, as_half8(xf), acc);
+          if (s & 1)
+            acc2 = mfma16x16x32(wf, as_half8(xf), acc2);
+          else
+            acc = mfma16x16x32(wf, as_half8(xf), acc);
         }
       }
+      // one group's operands at a time: unbounded hoisting of the X reads and the
+      // dequantization ahead of the MFMAs would spill
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
+  acc += acc2;
 
   __shared__ floatx4 red[4][64];
   red[wave][lane] = acc;
