@@ -528,7 +528,7 @@ __global__ __launch_bounds__(kThreads, kNorm ? 1 : 2) void gemv_kernel(Params p)
   u32x4 xv[kNorm ? 1 : 4 * kChunk];
   // X through a buffer descriptor over this workgroup's rows: lanes of rows past M use an
   // offset past the end and read zeros with no memory request and no branch (the host
-  // checks that the rows span less than 2^31 bytes)
+  // rejects calls whose 16 rows span more than 0x7ffffff0 bytes)
   const __amdgpu_buffer_rsrc_t xr_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(p.x + (int64_t)blockIdx.y * 16 * p.x_stride), (short)0,
       (int)(((int64_t)(rows_n - 1) * p.x_stride + p.K) * 2), 0x00020000);
@@ -930,9 +930,18 @@ int run_linear(const char* fn, const void* x, int64_t x_stride, int64_t M, int64
     set_error("%s: M %lld too large", fn, (long long)M);
     return FI_ERR_UNSUPPORTED;
   }
+  // the decode kernel addresses a workgroup's 16 X rows through one buffer descriptor whose
+  // size must stay below the offset its idle lanes use (0x7ffffff0)
+  const bool fused = norm && fuse_norm(M, K, pl);
+  const int64_t gemv_x_stride = norm && !fused ? K : x_stride;
+  if (pl.gemv_rows && (std::min<int64_t>(M, 16) - 1) * gemv_x_stride * 2 + K * 2 > 0x7ffffff0) {
+    set_error("%s: 16 rows of X span 2^31 bytes or more (x_stride %lld)", fn,
+              (long long)x_stride);
+    return FI_ERR_UNSUPPORTED;
+  }
   char* ws = (char*)workspace;
   Params p = make_params(x, x_stride, M, K, w, w_stride, scales, s_stride, N, out, out_stride);
-  if (norm && fuse_norm(M, K, pl)) {
+  if (fused) {
     p.norm_w = (const half_t*)norm_w;
     p.eps = eps;
     launch_linear<true>(p, int4, pl, nullptr, st);

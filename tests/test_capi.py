@@ -169,6 +169,10 @@ def test_int4_validation(lib):
                               None) == _lib.FI_ERR_INVALID
     assert lib.fi_int4_matmul(None, 256, 1, 256, 16, 128, 16, 2, 64, 128, 16, 64, None, 0,
                               None) == _lib.FI_ERR_INVALID
+    # decode-sized rows further apart than one 2^31-byte buffer descriptor covers
+    assert lib.fi_int4_matmul(16, 1 << 30, 2, 256, 16, 128, 16, 2, 64, 128, 16, 64, None, 0,
+                              None) == _lib.FI_ERR_UNSUPPORTED
+    assert b"2^31" in lib.fi_last_error()
     # a split call without its workspace is rejected before launch
     need = lib.fi_int4_matmul_workspace_size(40, 5120, 3072)
     assert need > 0
