@@ -54,20 +54,24 @@ __device__ __forceinline__ uint32_t as_u32(half2_t h) { return __builtin_bit_cas
 __device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
 
 // Eight int4 values (natural k order, nibble i = k0 + i) -> fp16(q * s).
+//
+// With e = d >> 4, byte j of e holds nibble 2j + 1 in its low half.  Two byte
+// permutations put byte j of d beside byte j of e, so that the low nibbles at bits 0 and
+// 16 are the k pairs (0, 1) and (4, 5), and 8 bits higher (2, 3) and (6, 7): every pair
+// comes out in MFMA order, with no permutation after the arithmetic (18 instructions).
 __device__ __forceinline__ half8 dequant8(uint32_t d, half2_t s2) {
 #pragma clang fp contract(off)
   d ^= 0x88888888u;  // two's complement nibble n -> n + 8 in [0, 15]
+  const uint32_t e = d >> 4;
+  const uint32_t lo = __builtin_amdgcn_perm(e, d, 0x05040100u);  // d.b0 d.b1 e.b0 e.b1
+  const uint32_t hi = __builtin_amdgcn_perm(e, d, 0x07060302u);  // d.b2 d.b3 e.b2 e.b3
   // 0x6400 | v is the fp16 value 1024 + v; minus 1032 gives the signed nibble exactly
   const half2_t bias = {(half_t)1032.0f, (half_t)1032.0f};
-  const half2_t p0 = (as_h2((d & 0x000F000Fu) | 0x64006400u) - bias) * s2;          // k0, k4
-  const half2_t p1 = (as_h2(((d >> 4) & 0x000F000Fu) | 0x64006400u) - bias) * s2;   // k1, k5
-  const half2_t p2 = (as_h2(((d >> 8) & 0x000F000Fu) | 0x64006400u) - bias) * s2;   // k2, k6
-  const half2_t p3 = (as_h2(((d >> 12) & 0x000F000Fu) | 0x64006400u) - bias) * s2;  // k3, k7
   u32x4 r;
-  r[0] = __builtin_amdgcn_perm(as_u32(p1), as_u32(p0), 0x05040100u);  // k0, k1
-  r[1] = __builtin_amdgcn_perm(as_u32(p3), as_u32(p2), 0x05040100u);  // k2, k3
-  r[2] = __builtin_amdgcn_perm(as_u32(p1), as_u32(p0), 0x07060302u);  // k4, k5
-  r[3] = __builtin_amdgcn_perm(as_u32(p3), as_u32(p2), 0x07060302u);  // k6, k7
+  r[0] = as_u32((as_h2((lo & 0x000F000Fu) | 0x64006400u) - bias) * s2);         // k0, k1
+  r[1] = as_u32((as_h2(((lo >> 8) & 0x000F000Fu) | 0x64006400u) - bias) * s2);  // k2, k3
+  r[2] = as_u32((as_h2((hi & 0x000F000Fu) | 0x64006400u) - bias) * s2);         // k4, k5
+  r[3] = as_u32((as_h2(((hi >> 8) & 0x000F000Fu) | 0x64006400u) - bias) * s2);  // k6, k7
   return as_half8(r);
 }
 
@@ -310,81 +314,126 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(Params p) {
 }
 
 // ---------------------------------------------------------------------------------------
-// Packed-weight GEMM for 17..64 rows, staged through direct-to-LDS copies.  The tile and
-// MFMA layout are gemm_kernel's (64 columns x MT rows per workgroup, 16 columns per wave,
-// one 128-wide K group per step), but each group's X tile (MT rows x 256 bytes) and W tile
-// (64 rows x 64 bytes) are copied global -> LDS with `buffer_load ... lds` into a ring of
-// three stages, two groups ahead of the MFMAs.  The copies hold no registers, so two
-// groups stay in flight while a third is multiplied; gemm_kernel keeps one group ahead in
-// registers and waits out most of a memory latency per group.
+// Packed-weight GEMM for 17..64 rows, staged through direct-to-LDS copies.  A workgroup
+// computes a 64-column x MT-row tile over a slice of the K groups with eight waves: wave
+// w = 4h + q takes columns 16q .. +15 of the groups t with t % 2 == h, so the SIMD's two
+// waves overlap one group's dequantization, LDS reads and MFMAs with the other's; the two
+// halves' sums are added through LDS at the end.  Each group's X tile (MT rows x 256
+// bytes) and W tile (64 rows x 64 bytes) are copied global -> LDS with `buffer_load ...
+// lds` into a ring of kDmaStages pairs of groups, two pairs ahead of the MFMAs; the copies
+// hold no registers.
 //
 // X rows sit in LDS unpadded, their 16-byte chunks XOR-permuted by row % 16 (the copy
 // lane that fills slot c of row r fetches chunk c ^ (r % 16)), so the 16 rows one MFMA
 // operand read touches fall on distinct banks.  X rows past M and weight rows past N read
 // zeros through the buffer bounds check.  The group scales of the workgroup's 64 columns
 // are staged in LDS once, at the start.
-constexpr int kDmaStages = 3;
+constexpr int kDmaThreads = 512;
+constexpr int kDmaStages = 3;      // pairs of groups in the ring
 constexpr int kDmaMaxGroups = 64;  // K groups per workgroup (one K split) the scale table holds
 
 template <int MT>
 struct DmaTile {
-  static constexpr int kXBytes = MT * 256;             // X tile of one group
-  static constexpr int kWBytes = kNTile * 64;          // W tile of one group (4 KiB)
+  static constexpr int kXBytes = MT * 256;     // X tile of one group
+  static constexpr int kWBytes = kNTile * 64;  // W tile of one group (4 KiB)
   static constexpr int kStage = kXBytes + kWBytes;
-  static constexpr int kXPerWave = kXBytes / 1024 / 4;  // X copies per wave per group
-  static constexpr int kIssue = kXPerWave + 1;          // copies per wave per group
+  static constexpr int kPair = 2 * kStage;
+  static constexpr int kCopies = kStage / 1024;  // 1 KiB copies per group: MT / 4 of X, 4 of W
+  static constexpr int kIssue = kCopies / 4;     // copies per wave per pair
+  static_assert(kCopies % 4 == 0, "the four waves of a half share a group's copies evenly");
+  // workgroups per CU the ring and scale table leave room for in 160 KiB of LDS
+  static constexpr int kLds = kDmaStages * kPair + kNTile * kDmaMaxGroups * 2;
+  static constexpr int kMinBlocks = 160 * 1024 / kLds >= 2 ? 2 : 1;
 };
 
-// This wave's copies of group g into `stage`: X slots wave * kXPerWave + q (1 KiB each,
-// X rows 4i..4i+3 of slot i) and W rows 16 * wave .. + 15.
+// The copies of one wave for the group pair it serves: copies (w % 4) * kIssue + i of its
+// half's group, X slots first (rows 4c .. 4c + 3 of slot c), then W slots (rows 16c .. +15).
+template <int MT>
+struct DmaCopies {
+  int voff[DmaTile<MT>::kIssue];  // per lane: byte offset in X or W at group 0
+  int lds[DmaTile<MT>::kIssue];   // byte offset of the copy in a group's stage
+  bool is_x[DmaTile<MT>::kIssue];
+};
+
+template <int MT>
+__device__ __forceinline__ DmaCopies<MT> dma_copies(const Params& p, int wave, int lane) {
+  using T = DmaTile<MT>;
+  DmaCopies<MT> c;
+#pragma unroll
+  for (int i = 0; i < T::kIssue; ++i) {
+    const int ci = (wave & 3) * T::kIssue + i;
+    c.is_x[i] = ci < MT / 4;
+    if (c.is_x[i]) {
+      const int r = 4 * ci + (lane >> 4);
+      c.voff[i] = r * (int)p.x_stride * 2 + (((lane & 15) ^ (r & 15)) << 4);
+      c.lds[i] = ci * 1024;
+    } else {
+      const int wi = ci - MT / 4;
+      c.voff[i] = (16 * wi + (lane >> 2)) * (int)p.w_stride + (lane & 3) * 16;
+      c.lds[i] = T::kXBytes + wi * 1024;
+    }
+  }
+  return c;
+}
+
+// This wave's copies of group g into the group's stage.
 template <int MT>
 __device__ __forceinline__ void dma_issue(rsrc_t xr, rsrc_t wr, char* stage, int g,
-                                          const int (&xoff)[DmaTile<MT>::kXPerWave], int woff,
-                                          int wave) {
+                                          const DmaCopies<MT>& c) {
   using T = DmaTile<MT>;
   const uint32_t base = lds_addr(stage);
 #pragma unroll
-  for (int q = 0; q < T::kXPerWave; ++q)
-    lds_copy16(xr, base + (wave * T::kXPerWave + q) * 1024, xoff[q], g * 256);
-  lds_copy16(wr, base + T::kXBytes + wave * 1024, woff, g * (kGroup / 2));
+  for (int i = 0; i < T::kIssue; ++i) {
+    if (c.is_x[i])
+      lds_copy16(xr, base + c.lds[i], c.voff[i], g * 256);
+    else
+      lds_copy16(wr, base + c.lds[i], c.voff[i], g * (kGroup / 2));
+  }
 }
 
 // One group's MFMAs from a resident stage: this lane's 16 weight bytes (k = 32 grp ..
-// +31 of its column) dequantized with the group's scale, against X rows 16 j + row.
+// +31 of column 16 q + row) dequantized with the group's scale, against X rows 16 j + row.
 template <int MT>
-__device__ __forceinline__ void dma_group(const char* stage, const half_t* sc, int t, int wave,
+__device__ __forceinline__ void dma_group(const char* stage, const half_t* sc, int t, int q,
                                           int row, int grp, floatx4 (&acc)[MT / 16]) {
   using T = DmaTile<MT>;
-  const u32x4 wv = *(const u32x4*)(stage + T::kXBytes + wave * 1024 + row * 64 + grp * 16);
-  const half_t s = sc[(16 * wave + row) * kDmaMaxGroups + t];
+  const u32x4 wv = *(const u32x4*)(stage + T::kXBytes + q * 1024 + row * 64 + grp * 16);
+  const half_t s = sc[(16 * q + row) * kDmaMaxGroups + t];
+  // every X fragment read goes out before the dequantization and the MFMAs, so one LDS
+  // latency covers them all
+  u32x4 xv[4][MT / 16];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int chunk = ((4 * grp + k) ^ row) << 4;
+#pragma unroll
+    for (int j = 0; j < MT / 16; ++j)
+      xv[k][j] = *(const u32x4*)(stage + (16 * j + row) * 256 + chunk);
+  }
+  __builtin_amdgcn_sched_barrier(0);
   const half2_t s2 = {s, s};
   half8 wf[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) wf[k] = dequant8(wv[k], s2);
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const int chunk = ((4 * grp + k) ^ row) << 4;
 #pragma unroll
-    for (int j = 0; j < MT / 16; ++j) {
-      const u32x4 xv = *(const u32x4*)(stage + (16 * j + row) * 256 + chunk);
-      acc[j] = mfma16x16x32(wf[k], as_half8(xv), acc[j]);
-    }
+    for (int j = 0; j < MT / 16; ++j) acc[j] = mfma16x16x32(wf[k], as_half8(xv[k][j]), acc[j]);
   }
 }
 
 template <int MT>
-__global__ __launch_bounds__(kThreads, 2) void gemm_dma_kernel(Params p) {
+__global__ __launch_bounds__(kDmaThreads, DmaTile<MT>::kMinBlocks) void gemm_dma_kernel(Params p) {
   using T = DmaTile<MT>;
   constexpr int kMSub = MT / 16;
-  // the ring's stages are distinct objects, so the compiler tracks each one's copies apart
-  __shared__ __attribute__((aligned(16))) char st0[T::kStage];
-  __shared__ __attribute__((aligned(16))) char st1[T::kStage];
-  __shared__ __attribute__((aligned(16))) char st2[T::kStage];
+  constexpr int S = kDmaStages;
+  static_assert(S >= 2 && S <= 3, "the step loop's wait covers 0..1 pairs ahead");
+  __shared__ __attribute__((aligned(16))) char ring[S * T::kPair];
   __shared__ half_t sc[kNTile * kDmaMaxGroups];
-  static_assert(kDmaStages == 3, "the step macro below rotates three stages");
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int h = wave >> 2;  // which group of each pair
+  const int q = wave & 3;   // which 16 columns
   const int row = lane & 15;
   const int grp = lane >> 4;
   const int n0 = blockIdx.x * kNTile;
@@ -392,56 +441,63 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_dma_kernel(Params p) {
   const int groups = p.K / kGroup;
   const int g_begin = blockIdx.z * p.groups_per_split;
   const int G = min(g_begin + p.groups_per_split, groups) - g_begin;  // <= 0: nothing to add
-
-  for (int f = threadIdx.x; f < kNTile * G; f += kThreads) {
-    const int col = f / G, t = f - col * G;
-    const int n = min(n0 + col, p.N - 1);
-    sc[col * kDmaMaxGroups + t] = p.scales[(int64_t)n * p.s_stride + g_begin + t];
-  }
-  __syncthreads();
+  const int P = (G + 1) / 2;                                          // group pairs
 
   const int rows_x = min(MT, p.M - m0);
   const int rows_w = min(kNTile, p.N - n0);
   const rsrc_t xr =
       raw_rsrc(p.x + (int64_t)m0 * p.x_stride, (int)((rows_x - 1) * p.x_stride * 2 + p.K * 2));
   const rsrc_t wr = raw_rsrc(p.w + (int64_t)n0 * p.w_stride, (int)((rows_w - 1) * p.w_stride + p.K / 2));
-  int xoff[T::kXPerWave];
+  const DmaCopies<MT> cp = dma_copies<MT>(p, wave, lane);
+
+  // The first S - 1 pairs' copies go out before the scale table is read, so the two
+  // latencies overlap.  The compiler waits for the scale loads (and with them for every
+  // copy issued before them) before writing the table; step 0's barrier publishes it.
+  // A pair's second group past the split (odd G) is copied like the others (the buffer
+  // bounds keep it in range) and never multiplied.
 #pragma unroll
-  for (int q = 0; q < T::kXPerWave; ++q) {
-    const int r = 4 * (wave * T::kXPerWave + q) + (lane >> 4);
-    xoff[q] = r * (int)p.x_stride * 2 + (((lane & 15) ^ (r & 15)) << 4);
+  for (int u = 0; u < S - 1; ++u)
+    if (u < P) dma_issue<MT>(xr, wr, ring + u * T::kPair + h * T::kStage, g_begin + 2 * u + h, cp);
+  for (int f = threadIdx.x; f < kNTile * G; f += kDmaThreads) {
+    const int col = f / G, t = f - col * G;
+    const int n = min(n0 + col, p.N - 1);
+    sc[col * kDmaMaxGroups + t] = p.scales[(int64_t)n * p.s_stride + g_begin + t];
   }
-  const int woff = (16 * wave + (lane >> 2)) * (int)p.w_stride + (lane & 3) * 16;
 
   floatx4 acc[kMSub];
 #pragma unroll
   for (int j = 0; j < kMSub; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  if (G > 0) dma_issue<MT>(xr, wr, st0, g_begin, xoff, woff, wave);
-  if (G > 1) dma_issue<MT>(xr, wr, st1, g_begin + 1, xoff, woff, wave);
-  // Step t: wait for group t's copies (group t + 1's may still be in flight), barrier (so
-  // every wave's copies of group t have landed and every wave is done with group t - 1's
-  // stage), refill that stage with group t + 2, multiply group t.
-#define FI_DMA_STEP(TT, CUR, NXT)                                                 \
-  {                                                                               \
-    if ((TT) + 1 < G)                                                             \
-      wait_vmcnt<T::kIssue>();                                                    \
-    else                                                                          \
-      wait_vmcnt<0>();                                                            \
-    __builtin_amdgcn_s_barrier();                                                 \
-    if ((TT) + 2 < G) dma_issue<MT>(xr, wr, NXT, g_begin + (TT) + 2, xoff, woff, wave); \
-    dma_group<MT>(CUR, sc, (TT), wave, row, grp, acc);                            \
+  // Step u: wait for this wave's copies of pair u (the pair after it may still be in
+  // flight), barrier (every wave's copies of pair u have landed, every wave is done with
+  // pair u - 1's stage), refill that stage with pair u + S - 1, multiply this half's group.
+  for (int u = 0; u < P; ++u) {
+    if (u + 1 < P && S > 2)
+      wait_vmcnt<T::kIssue>();
+    else
+      wait_vmcnt<0>();
+    wait_lgkmcnt0();  // the scale table's LDS writes (step 0)
+    __builtin_amdgcn_s_barrier();
+    if (u + S - 1 < P)
+      dma_issue<MT>(xr, wr, ring + ((u + S - 1) % S) * T::kPair + h * T::kStage,
+                    g_begin + 2 * (u + S - 1) + h, cp);
+    if (2 * u + h < G)
+      dma_group<MT>(ring + (u % S) * T::kPair + h * T::kStage, sc, 2 * u + h, q, row, grp, acc);
   }
-  for (int t = 0; t < G; t += 3) {
-    FI_DMA_STEP(t, st0, st2)
-    if (t + 1 >= G) break;
-    FI_DMA_STEP(t + 1, st1, st0)
-    if (t + 2 >= G) break;
-    FI_DMA_STEP(t + 2, st2, st1)
-  }
-#undef FI_DMA_STEP
 
-  store_tile<kMSub>(p, acc, m0, n0);
+  // the second half's sums join the first half's through the (now idle) ring
+  floatx4* red = (floatx4*)ring;
+  __syncthreads();
+  if (h == 1) {
+#pragma unroll
+    for (int j = 0; j < kMSub; ++j) red[(q * kMSub + j) * 64 + lane] = acc[j];
+  }
+  __syncthreads();
+  if (h == 0) {
+#pragma unroll
+    for (int j = 0; j < kMSub; ++j) acc[j] += red[(q * kMSub + j) * 64 + lane];
+    store_tile<kMSub>(p, acc, m0, n0);
+  }
 }
 
 // Prefill-sized calls: the MFMA kernels above spend most of their time dequantizing (each
@@ -835,9 +891,9 @@ void launch_linear(const fi::gemm::Params& base, bool int4, const fi::gemm::Plan
   } while (0)
   if (int4 && dma_ok(p, pl)) {
     if (pl.mt == 32)
-      hipLaunchKernelGGL(gemm_dma_kernel<32>, grid, dim3(kThreads), 0, st, p);
+      hipLaunchKernelGGL(gemm_dma_kernel<32>, grid, dim3(kDmaThreads), 0, st, p);
     else
-      hipLaunchKernelGGL(gemm_dma_kernel<64>, grid, dim3(kThreads), 0, st, p);
+      hipLaunchKernelGGL(gemm_dma_kernel<64>, grid, dim3(kDmaThreads), 0, st, p);
   } else {
     switch (pl.mt) {
       case 16: FI_GEMM_LAUNCH(16); break;
