@@ -682,16 +682,35 @@ __global__ __launch_bounds__(kThreads, kNorm ? 1 : 2) void gemv_kernel(Params p)
 }
 
 // out[m, n] = fp16(sum over splits of partial[s, m, n]), splits added in order.
+template <int V>
 __global__ __launch_bounds__(256) void reduce_kernel(const float* partial, int splits, int M,
                                                      int N, half_t* out, int64_t out_stride) {
+  // V consecutive outputs of one row per thread (V = 4: N % 4 == 0 and 8-byte aligned output
+  // rows).  The partials of up to 8 splits are loaded before any is added, so one memory
+  // latency covers them; the sum runs in split order from 0.f either way.
+  typedef float fv __attribute__((ext_vector_type(V)));
   const int64_t total = (int64_t)M * N;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    float s = 0.f;
-    for (int k = 0; k < splits; ++k) s += __builtin_nontemporal_load(partial + k * total + i);
+  for (int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * V; i < total;
+       i += (int64_t)gridDim.x * blockDim.x * V) {
+    fv s = {};
+    for (int k0 = 0; k0 < splits; k0 += 8) {
+      fv v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (k0 + k < splits)
+          v[k] = __builtin_nontemporal_load((const fv*)(partial + (k0 + k) * total + i));
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (k0 + k < splits) s += v[k];
+    }
     const int m = (int)(i / N);
     const int nn = (int)(i - (int64_t)m * N);
-    out[(int64_t)m * out_stride + nn] = (half_t)s;
+    half_t* dst = out + (int64_t)m * out_stride + nn;
+    if constexpr (V == 4) {
+      *(half4*)dst = to_half4(s);
+    } else {
+      dst[0] = (half_t)s[0];
+    }
   }
 }
 
@@ -905,9 +924,14 @@ void launch_linear(const fi::gemm::Params& base, bool int4, const fi::gemm::Plan
 #undef FI_GEMM_LAUNCH
   if (pl.splits > 1) {
     const int64_t total = (int64_t)p.M * p.N;
-    const int64_t blocks = std::min<int64_t>((total + 255) / 256, 4096);
-    hipLaunchKernelGGL(reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
-                       (const float*)workspace, pl.splits, p.M, p.N, p.out, p.out_stride);
+    const bool v4 = p.N % 4 == 0 && p.out_stride % 4 == 0 && ((uintptr_t)p.out & 7) == 0;
+    const int64_t blocks = std::min<int64_t>((total / (v4 ? 4 : 1) + 255) / 256, 4096);
+    if (v4)
+      hipLaunchKernelGGL(reduce_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, st,
+                         (const float*)workspace, pl.splits, p.M, p.N, p.out, p.out_stride);
+    else
+      hipLaunchKernelGGL(reduce_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, st,
+                         (const float*)workspace, pl.splits, p.M, p.N, p.out, p.out_stride);
   }
 }
 
