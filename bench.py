@@ -385,8 +385,18 @@ def bench_int4(torch, fi, timer, steps, warmup, dev):
                 fi.int4_matmul(x, wo, workspace=ws)
 
         t = timer.run(step, max(1, steps // 10), max(1, warmup // 5))
+        # the same 56 calls captured once and replayed as one HIP graph (no host launch
+        # cost between kernels; the workspace is the explicit one above)
+        step()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        t_graph = timer.run(graph.replay, max(1, steps // 10), max(1, warmup // 5))
+        del graph
         nbytes = L * (R.int4_matmul_bytes(M, NQKV, K) + R.int4_matmul_bytes(M, NO, K))
-        res[f"decode_b{M}"] = dict(t=t, bytes=nbytes, gbs=nbytes / t / 1e9)
+        res[f"decode_b{M}"] = dict(t=t, bytes=nbytes, gbs=nbytes / t / 1e9, t_graph=t_graph,
+                                   gbs_graph=nbytes / t_graph / 1e9)
     # RMSNorm (model.py:82) fused with the QKV projection against the two-step form
     nws = [(torch.randn(K, device=dev, generator=g) * 0.1 + 1).half() for _ in range(L)]
     for M in (1, 64):
@@ -615,10 +625,14 @@ def main():
                         "tokens",
             "decode_b64": {"us_per_layer": round(d64["t"] / 28 * 1e6, 2),
                            "GB/s": round(d64["gbs"], 1),
-                           "frac_hbm": round(d64["gbs"] / R.HBM_PEAK_GBS, 4)},
+                           "frac_hbm": round(d64["gbs"] / R.HBM_PEAK_GBS, 4),
+                           "graph_us_per_layer": round(d64["t_graph"] / 28 * 1e6, 2),
+                           "graph_GB/s": round(d64["gbs_graph"], 1)},
             "decode_b1": {"us_per_layer": round(d1["t"] / 28 * 1e6, 2),
                           "GB/s": round(d1["gbs"], 1),
-                          "frac_hbm": round(d1["gbs"] / R.HBM_PEAK_GBS, 4)},
+                          "frac_hbm": round(d1["gbs"] / R.HBM_PEAK_GBS, 4),
+                          "graph_us_per_layer": round(d1["t_graph"] / 28 * 1e6, 2),
+                          "graph_GB/s": round(d1["gbs_graph"], 1)},
             "prefill_qkv_m16384": {"us_per_call": round(pq["t"] * 1e6, 1),
                                    "TFLOP/s": round(pq["tflops"], 1),
                                    "frac_mfma": round(pq["tflops"] / R.FP16_MFMA_PEAK_TFLOPS, 4)},
@@ -630,8 +644,9 @@ def main():
                                 "GB/s": round(q["rms_norm_prefill"]["gbs"], 1),
                                 "frac_hbm": round(q["rms_norm_prefill"]["gbs"] / R.HBM_PEAK_GBS,
                                                   4)}}
-        print(f"[bench] int4 decode b64 {d64['t'] / 28 * 1e6:.2f} us/layer {d64['gbs']:.0f} GB/s; "
-              f"b1 {d1['t'] / 28 * 1e6:.2f} us/layer {d1['gbs']:.0f} GB/s; prefill qkv "
+        print(f"[bench] int4 decode b64 {d64['t'] / 28 * 1e6:.2f} us/layer {d64['gbs']:.0f} GB/s "
+              f"(graph {d64['t_graph'] / 28 * 1e6:.2f}); b1 {d1['t'] / 28 * 1e6:.2f} us/layer "
+              f"{d1['gbs']:.0f} GB/s (graph {d1['t_graph'] / 28 * 1e6:.2f}); prefill qkv "
               f"{pq['t'] * 1e6:.0f} us {pq['tflops']:.0f} TFLOP/s", file=sys.stderr, flush=True)
         print("[bench] norm+qkv fused/two-step us: " + ", ".join(
             f"b{M} {q[f'norm_qkv_b{M}']['fused'] * 1e6:.2f}/{q[f'norm_qkv_b{M}']['two_step'] * 1e6:.2f}"
