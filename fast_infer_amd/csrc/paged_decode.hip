@@ -189,15 +189,9 @@ __global__ __launch_bounds__(256, 2) void partition_kernel(Params p) {
 
   const int ctx = row_context(p, b);
   const int split_start = split * p.tokens_per_split;
-  if (!p.direct && split_start >= ctx) {
-    // no tokens here: leave an empty partial (m = kNegBig, l = 0) for the merge
-    if (threadIdx.x < p.heads_per_wg) {
-      const int64_t slot = ((int64_t)b * p.num_q_heads + head0 + threadIdx.x) * p.max_splits + split;
-      p.part_ml[slot * 2 + 0] = kNegBig;
-      p.part_ml[slot * 2 + 1] = 0.f;
-    }
-    return;
-  }
+  // no tokens here: the merge reads only the row's first ceil(ctx / tokens_per_split)
+  // partials, so this partition writes nothing
+  if (!p.direct && split_start >= ctx) return;
   const int split_end = min(split_start + p.tokens_per_split, ctx);
 
   // Block-table entries of this partition, validated once, staged in LDS.
@@ -325,21 +319,23 @@ __global__ __launch_bounds__(256, 2) void partition_kernel(Params p) {
 }
 
 // Merge the partition partials of one (row, query head): o = sum_s e^(m_s-M) o_s /
-// sum_s e^(m_s-M) l_s, zeros for an empty row.  Every partition of the row wrote a
-// partial (empty ones: m = kNegBig, l = 0), so all loads are issued at once with no
-// dependency on the row's length; empty partials are selected away, never multiplied.
+// sum_s e^(m_s-M) l_s, zeros for an empty row.  The row's length gives its partition
+// count (the partitions past it wrote nothing); those partials' loads are issued at
+// once, and partials with l = 0 (no valid key) are selected away, never multiplied.
 __global__ __launch_bounds__(kHeadDim) void merge_kernel(Params p) {
   constexpr int kBatch = 16;  // partials loaded per round (one round for up to 16 partitions)
   const int h = blockIdx.x;
   const int b = blockIdx.y;
   const int d = threadIdx.x;
   const int64_t slot0 = ((int64_t)b * p.num_q_heads + h) * p.max_splits;
+  const int ctx = row_context(p, b);
+  const int nparts = min((ctx + p.tokens_per_split - 1) / p.tokens_per_split, p.max_splits);
   float mx = kNegBig, L = 0.f, O = 0.f;
-  for (int s0 = 0; s0 < p.max_splits; s0 += kBatch) {
+  for (int s0 = 0; s0 < nparts; s0 += kBatch) {
     float m[kBatch], l[kBatch], o[kBatch];
 #pragma unroll
     for (int k = 0; k < kBatch; ++k) {
-      const int s = s0 + k < p.max_splits ? s0 + k : p.max_splits - 1;
+      const int s = s0 + k < nparts ? s0 + k : nparts - 1;
       // read once: non-temporal
       m[k] = __builtin_nontemporal_load(p.part_ml + (slot0 + s) * 2);
       l[k] = __builtin_nontemporal_load(p.part_ml + (slot0 + s) * 2 + 1);
@@ -347,7 +343,7 @@ __global__ __launch_bounds__(kHeadDim) void merge_kernel(Params p) {
     }
 #pragma unroll
     for (int k = 0; k < kBatch; ++k) {
-      const bool use = s0 + k < p.max_splits && l[k] > 0.f;
+      const bool use = s0 + k < nparts && l[k] > 0.f;
       const float mk = use ? m[k] : kNegBig;
       const float mn = fmaxf(mx, mk);
       const float a = fast_exp2(mx - mn);
