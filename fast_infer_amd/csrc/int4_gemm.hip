@@ -550,13 +550,13 @@ inline int blas_gemm(const half_t* x, int64_t ldx, const half_t* w, int64_t ldw,
 }
 
 // Decode-sized calls (16 rows of X per blockIdx.y): one workgroup per 16 output columns.
-// The four waves take interleaved groups (g = wave, wave + 4, ...), so K is split inside
+// The kW waves take interleaved groups (g = wave, wave + kW, ...), so K is split inside
 // the workgroup and no partials leave it.  Each lane issues the loads of kChunk groups at
 // once (16 weight bytes, the scale, and 64 bytes of its X row per group) before any math,
-// so one memory latency covers the chunk; the four waves' sums are added through LDS in
+// so one memory latency covers the chunk; the kW waves' sums are added through LDS in
 // a fixed order.
-template <bool kInt4, int kChunk, bool kNorm>
-__global__ __launch_bounds__(kThreads, kNorm ? 1 : 2) void gemv_kernel(Params p) {
+template <bool kInt4, int kChunk, bool kNorm, int kW>
+__global__ __launch_bounds__(64 * kW, kNorm ? 1 : 2) void gemv_kernel(Params p) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int row = lane & 15;
@@ -576,7 +576,7 @@ __global__ __launch_bounds__(kThreads, kNorm ? 1 : 2) void gemv_kernel(Params p)
   const int rows_n = min(16, p.M - (int)blockIdx.y * 16);
   const half_t* xrow_n = xn + min(row, rows_n - 1) * p.K;
 
-  // Issue the loads of one chunk (kChunk groups of this wave, g0, g0 + 4, ...): every load
+  // Issue the loads of one chunk (kChunk groups of this wave, g0, g0 + kW, ...): every load
   // goes out before any math and without branches (groups past the end reload the last
   // group and are skipped), so one latency covers the chunk.
   u32x4 wv[kInt4 ? kChunk : 4 * kChunk];
@@ -592,7 +592,7 @@ __global__ __launch_bounds__(kThreads, kNorm ? 1 : 2) void gemv_kernel(Params p)
   auto load_chunk = [&](int g0) {
 #pragma unroll
     for (int c = 0; c < kChunk; ++c) {
-      const int g = min(g0 + 4 * c, groups - 1);
+      const int g = min(g0 + kW * c, groups - 1);
       if constexpr (kInt4) {
         wv[c] = *(const u32x4*)(p.w + (int64_t)nc * p.w_stride + g * (kGroup / 2) + grp * 16);
         sv[c] = p.scales[(int64_t)nc * p.s_stride + g];
@@ -617,7 +617,7 @@ __global__ __launch_bounds__(kThreads, kNorm ? 1 : 2) void gemv_kernel(Params p)
   load_chunk(wave);
   __builtin_amdgcn_sched_barrier(0);
   if constexpr (kNorm) {
-    for (int r = wave; r < rows_n; r += 4)
+    for (int r = wave; r < rows_n; r += kW)
       norm_row_to(p.x + (int64_t)(blockIdx.y * 16 + r) * p.x_stride, p.norm_w, p.K, p.eps,
                   xn + r * p.K, lane);
     __syncthreads();
@@ -626,14 +626,14 @@ __global__ __launch_bounds__(kThreads, kNorm ? 1 : 2) void gemv_kernel(Params p)
   // two accumulators, alternating by k-step, halve the chain of dependent MFMAs
   floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
   floatx4 acc2 = floatx4{0.f, 0.f, 0.f, 0.f};
-  for (int g0 = wave; g0 < groups; g0 += 4 * kChunk) {
+  for (int g0 = wave; g0 < groups; g0 += kW * kChunk) {
     if (g0 != wave) {
       load_chunk(g0);
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int c = 0; c < kChunk; ++c) {
-      if (g0 + 4 * c < groups) {  // uniform across the wave
+      if (g0 + kW * c < groups) {  // uniform across the wave
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
           half8 wf;
@@ -643,7 +643,7 @@ __global__ __launch_bounds__(kThreads, kNorm ? 1 : 2) void gemv_kernel(Params p)
             wf = as_half8(wv[4 * c + s]);
           u32x4 xf;
           if constexpr (kNorm)
-            xf = *(const u32x4*)(xrow_n + (g0 + 4 * c) * kGroup + grp * 32 + 8 * s);
+            xf = *(const u32x4*)(xrow_n + (g0 + kW * c) * kGroup + grp * 32 + 8 * s);
           else
             xf = xv[4 * c + s];
           if (s & 1)
@@ -659,13 +659,13 @@ __global__ __launch_bounds__(kThreads, kNorm ? 1 : 2) void gemv_kernel(Params p)
   }
   acc += acc2;
 
-  __shared__ floatx4 red[4][64];
+  __shared__ floatx4 red[kW][64];
   red[wave][lane] = acc;
   __syncthreads();
   if (wave == 0) {
     floatx4 t = red[0][lane];
 #pragma unroll
-    for (int w = 1; w < 4; ++w) t += red[w][lane];
+    for (int w = 1; w < kW; ++w) t += red[w][lane];
     if (m_ok) {
       const int nb = n0 + 4 * grp;
       half_t* dst = p.out + (int64_t)m * p.out_stride + nb;
@@ -890,10 +890,14 @@ void launch_linear(const fi::gemm::Params& base, bool int4, const fi::gemm::Plan
     p.groups_per_split = p.K / kGroup;
     const dim3 grid((unsigned)((p.N + 15) / 16), (unsigned)((p.M + 15) / 16), 1);
     const size_t lds = kNorm ? (size_t)std::min(p.M, 16) * p.K * sizeof(half_t) : 0;
-    if (int4)
-      hipLaunchKernelGGL((gemv_kernel<true, 6, kNorm>), grid, dim3(kThreads), lds, st, p);
+    // packed weights: eight waves (two per SIMD hide the dequantization's VALU latency),
+    // except with the fused norm, whose registers allow only one such workgroup per CU
+    if (int4 && !kNorm)
+      hipLaunchKernelGGL((gemv_kernel<true, 3, false, 8>), grid, dim3(512), lds, st, p);
+    else if (int4)
+      hipLaunchKernelGGL((gemv_kernel<true, 6, kNorm, 4>), grid, dim3(kThreads), lds, st, p);
     else
-      hipLaunchKernelGGL((gemv_kernel<false, 3, kNorm>), grid, dim3(kThreads), lds, st, p);
+      hipLaunchKernelGGL((gemv_kernel<false, 3, kNorm, 4>), grid, dim3(kThreads), lds, st, p);
     return;
   }
   p.partial = pl.splits > 1 ? (float*)workspace : nullptr;
