@@ -182,10 +182,16 @@ __global__ __launch_bounds__(256, 2) void partition_kernel(Params p) {
   const int col = lane & 15;  // MFMA column: query head within the workgroup
   const int g = lane >> 4;    // 16-lane row of the wave
   const int hgroups_per_kv = p.group / p.heads_per_wg;
-  const int kvh = blockIdx.x / hgroups_per_kv;
-  const int head0 = kvh * p.group + (blockIdx.x % hgroups_per_kv) * p.heads_per_wg;
   const int split = blockIdx.y;
   const int b = blockIdx.z;
+  // Head group of this workgroup, rotated by partition and row.  The hardware deals
+  // consecutive workgroups to the XCDs in turn, so with gridDim.x = 8 XCD k would read head
+  // group k of every (row, partition).  The head slices of a pool row do not all stream
+  // equally fast, and the XCDs serving the slow ones would finish last; rotated, every XCD
+  // serves every head group equally often.
+  const int hg = (int)((blockIdx.x + blockIdx.y + blockIdx.z) % gridDim.x);
+  const int kvh = hg / hgroups_per_kv;
+  const int head0 = kvh * p.group + (hg % hgroups_per_kv) * p.heads_per_wg;
 
   const int ctx = row_context(p, b);
   const int split_start = split * p.tokens_per_split;
