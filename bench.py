@@ -48,9 +48,10 @@ HQ, HKV, D, BS = 24, 8, 128, 64
 # MFMA-bound kernels (prefill attention, the prefill GEMM) run 10-20% slower over their
 # first few tens of milliseconds of back-to-back calls (same tensors; a GEMM load
 # beforehand does not remove it), and on a GPU that has just been idle a 0.1 s warm-up
-# still left the first process's prefill about 4% slower than a second process's; their
-# sections keep calling, untimed, for this long before timing.
-MFMA_WARM_S = 0.5
+# still left the first process's prefill about 4% slower than a second process's.  The
+# batch-32 decode, the first section a process times, runs 3-7% slower over its first
+# hundred calls too.  These sections keep calling, untimed, for this long before timing.
+WARM_S = 0.5
 
 
 def _args():
@@ -149,7 +150,7 @@ def bench_decode_b32(torch, fi, timer, steps, warmup, dev):
         it[0] += 1
         fi.paged_attention(q, kc, vc, table, BS, 4096, context_lens=cl, workspace=ws)
 
-    t = timer.run(step, steps, warmup)
+    t = timer.run(step, steps, warmup, WARM_S)
     nbytes = R.decode_bytes(lens, HQ, HKV, D, BS)
     gbs = nbytes / t / 1e9
     return dict(t=t, bytes=nbytes, gbs=gbs, lens=lens, q=q, pools=pools[0], table=table)
@@ -420,7 +421,7 @@ def bench_int4(torch, fi, timer, steps, warmup, dev):
     res["rms_norm_prefill"] = dict(t=t, bytes=nbytes, gbs=nbytes / t / 1e9)
     wqkv = layers[0][0]
     t = timer.run(lambda: fi.int4_matmul(x, wqkv), max(1, steps // 10), max(1, warmup // 5),
-                  MFMA_WARM_S)
+                  WARM_S)
     fl = R.matmul_flops(M, NQKV, K)
     res["prefill_qkv"] = dict(t=t, flops=fl, tflops=fl / t / 1e12)
     return res
@@ -524,7 +525,7 @@ def main():
     pre_steps, pre_warm = max(1, steps // 5), max(1, warm // 2)
     if "prefill" in only:
         pre = bench_prefill(torch, fi, timer, pre_steps, pre_warm, dev, 4, 4096, 256, 3,
-                            warm_s=MFMA_WARM_S)
+                            warm_s=WARM_S)
         print(f"[bench] prefill b4 s4096: {pre['t'] * 1e6:.1f} us/call, "
               f"{pre['tflops']:.1f} TFLOP/s", file=sys.stderr, flush=True)
 
@@ -552,7 +553,7 @@ def main():
                         "with the K/V write into a 256-block pool (block_size 64)",
             "value": round(pre["tflops"], 2), "unit": "TFLOP/s",
             "ms_per_step": round(pre["t"] * 1e3, 5), "steps": pre_steps, "warmup": pre_warm,
-            "warm_s": MFMA_WARM_S,
+            "warm_s": WARM_S,
             "roofline": {"bound": "mfma", "achieved": round(pre["tflops"], 2),
                          "peak": R.FP16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(pre["tflops"] / R.FP16_MFMA_PEAK_TFLOPS, 4),
@@ -562,7 +563,7 @@ def main():
         }
     if "small" in only:
         d1 = bench_decode_b1(torch, fi, timer, steps, warm, dev)
-        p1 = bench_prefill(torch, fi, timer, steps, warm, dev, 1, 512, 64, 1, warm_s=MFMA_WARM_S)
+        p1 = bench_prefill(torch, fi, timer, steps, warm, dev, 1, 512, 64, 1, warm_s=WARM_S)
         out["decode_b1_ctx256"] = {"us_per_call": round(d1["t"] * 1e6, 2),
                                    "GB/s": round(d1["gbs"], 1), "bytes": d1["bytes"]}
         out["prefill_b1_s512"] = {"us_per_call": round(p1["t"] * 1e6, 2),
