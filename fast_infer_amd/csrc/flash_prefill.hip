@@ -483,17 +483,37 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(Params p) {
   }
 #undef FI_PREFILL_STEP
 
-  // ---- normalise and store: lane holds O[qpos][16*dt + 4*g + r].  The row sums
-  // combine lanes of the same column, which share qpos, so the branch is uniform
-  // across every shuffle's partners.
-  if (qpos < p.seq_len) {
+  // ---- normalise and store: lane holds O[qpos][16*dt + 4*g + r].  The row sums combine
+  // the four lanes of a column (every lane takes part; rows past seq_len are never stored).
+  // The rows go through this wave's own part of the tile stages, idle since the last
+  // barrier, so that each store instruction writes four whole 256-byte rows (16 lanes x 16
+  // bytes per row) rather than 32-byte pieces of sixteen rows: a workgroup's slot is held
+  // until its last stores complete.  Staged rows are padded to 272 bytes so that the
+  // sixteen rows of one write land in distinct banks.
+  constexpr int kORow = 272;
+  static_assert(kWaves == 4 && 2 * HPW * kRowsPerWave * kORow <= kStageBytes,
+                "waves 0-1 stage their rows in st0, waves 2-3 in st1");
+  char* ostage = (w < 2 ? st0 : st1) + (w & 1) * (HPW * kRowsPerWave * kORow);
 #pragma unroll
-    for (int j = 0; j < HPW; ++j) {
-      const float inv = 1.f / row4_sum(l_run[j]);
-      half_t* orow = p.o + (int64_t)b * p.o_sb + (int64_t)(head0 + j) * p.o_sh +
-                     (int64_t)qpos * p.o_ss + 4 * g;
+  for (int j = 0; j < HPW; ++j) {
+    const float inv = 1.f / row4_sum(l_run[j]);
+    char* orow = ostage + (j * kRowsPerWave + col) * kORow + 8 * g;
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) *(half4*)(orow + 16 * dt) = to_half4(acc[j][dt] * inv);
+    for (int dt = 0; dt < 8; ++dt) *(half4*)(orow + 32 * dt) = to_half4(acc[j][dt] * inv);
+  }
+  wave_lds_sync();
+  const int r4 = lane >> 4;   // row within each group of four read by one instruction
+  const int c16 = lane & 15;  // 16-byte chunk of the row
+#pragma unroll
+  for (int j = 0; j < HPW; ++j) {
+#pragma unroll
+    for (int rr = 0; rr < kRowsPerWave / 4; ++rr) {
+      const int rl = 4 * rr + r4;
+      const u32x4 v = *(const u32x4*)(ostage + (j * kRowsPerWave + rl) * kORow + 16 * c16);
+      const int pos = q0 + kRowsPerWave * w + rl;
+      if (pos < p.seq_len)
+        *(u32x4*)(p.o + (int64_t)b * p.o_sb + (int64_t)(head0 + j) * p.o_sh +
+                  (int64_t)pos * p.o_ss + 8 * c16) = v;
     }
   }
 }
