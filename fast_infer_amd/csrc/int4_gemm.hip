@@ -76,6 +76,31 @@ __device__ __forceinline__ half8 dequant8(uint32_t d, half2_t s2) {
   return as_half8(r);
 }
 
+// Store C[m][nb .. nb + 3] (columns past N dropped): to the fp32 partials of split
+// blockIdx.z, or as fp16 to the output.
+__device__ __forceinline__ void store_row_piece(const Params& p, floatx4 v, int m, int nb) {
+  if (p.partial) {
+    float* dst = p.partial + ((int64_t)blockIdx.z * p.M + m) * p.N + nb;
+    if (nb + 3 < p.N && (p.N & 3) == 0) {
+      *(floatx4*)dst = v;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (nb + i < p.N) dst[i] = v[i];
+    }
+  } else {
+    half_t* dst = p.out + (int64_t)m * p.out_stride + nb;
+    const half4 h = to_half4(v);
+    if (nb + 3 < p.N && ((uintptr_t)dst & 7) == 0) {
+      *(half4*)dst = h;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (nb + i < p.N) dst[i] = h[i];
+    }
+  }
+}
+
 // Store a workgroup's 64-column x (16 * kMSub)-row tile.  Lane (row, grp) of wave w holds
 // C[m0 + 16j + row][n0 + 16w + 4grp + i] in acc[j][i].  With K split over blockIdx.z the
 // tile goes to the fp32 partials (reduce_kernel adds them), otherwise to the fp16 output.
@@ -89,27 +114,7 @@ __device__ __forceinline__ void store_tile(const Params& p, const floatx4 (&acc)
 #pragma unroll
   for (int j = 0; j < kMSub; ++j) {
     const int m = m0 + 16 * j + row;
-    if (m >= p.M) continue;
-    if (p.partial) {
-      float* dst = p.partial + ((int64_t)blockIdx.z * p.M + m) * p.N + nb;
-      if (nb + 3 < p.N && (p.N & 3) == 0) {
-        *(floatx4*)dst = acc[j];
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (nb + i < p.N) dst[i] = acc[j][i];
-      }
-    } else {
-      half_t* dst = p.out + (int64_t)m * p.out_stride + nb;
-      const half4 h = to_half4(acc[j]);
-      if (nb + 3 < p.N && ((uintptr_t)dst & 7) == 0) {
-        *(half4*)dst = h;
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (nb + i < p.N) dst[i] = h[i];
-      }
-    }
+    if (m < p.M) store_row_piece(p, acc[j], m, nb);
   }
 }
 
@@ -494,10 +499,29 @@ __global__ __launch_bounds__(kDmaThreads, DmaTile<MT>::kMinBlocks) void gemm_dma
     for (int j = 0; j < kMSub; ++j) red[(q * kMSub + j) * 64 + lane] = acc[j];
   }
   __syncthreads();
+  // The finished tile is staged after the reduction area, rows padded to 272 bytes, and
+  // written out row by row: 16 consecutive lanes store one row's 64 columns, where each
+  // lane's own accumulators would give 64-byte pieces of 16 rows (the workgroup's slot is
+  // held until its last stores complete).
+  constexpr int kTRow = 272;
+  char* tile = ring + 4 * kMSub * 64 * (int)sizeof(floatx4);
+  static_assert(4 * kMSub * 64 * sizeof(floatx4) + MT * kTRow <= S * T::kPair,
+                "the staged tile fits the ring");
+  static_assert(MT * 16 % kDmaThreads == 0, "whole rounds of row pieces");
   if (h == 0) {
 #pragma unroll
-    for (int j = 0; j < kMSub; ++j) acc[j] += red[(q * kMSub + j) * 64 + lane];
-    store_tile<kMSub>(p, acc, m0, n0);
+    for (int j = 0; j < kMSub; ++j) {
+      acc[j] += red[(q * kMSub + j) * 64 + lane];
+      *(floatx4*)(tile + (16 * j + row) * kTRow + (16 * q + 4 * grp) * 4) = acc[j];
+    }
+  }
+  __syncthreads();
+  const int rows = min(MT, p.M - m0);
+#pragma unroll
+  for (int it = 0; it < MT * 16 / kDmaThreads; ++it) {
+    const int idx = threadIdx.x + kDmaThreads * it;
+    const int r = idx >> 4, c = idx & 15;
+    if (r < rows) store_row_piece(p, *(const floatx4*)(tile + r * kTRow + 16 * c), m0 + r, n0 + 4 * c);
   }
 }
 
@@ -785,8 +809,10 @@ struct Plan {
 // up to 16 rows, the tiled split-K kernels up to 128, the library GEMM above.
 constexpr int kGemvMaxM = 16;
 constexpr int kLibraryMinM = 129;
+constexpr int kCus = 256;  // MI355X compute units
 
-inline Plan plan(int64_t M, int64_t N, int64_t K) {
+// int4: packed weights, whose 64-row tiles run gemm_dma_kernel<64> at one workgroup per CU.
+inline Plan plan(int64_t M, int64_t N, int64_t K, bool int4) {
   Plan pl;
   pl.gemv_rows = 0;
   pl.library = false;
@@ -811,6 +837,10 @@ inline Plan plan(int64_t M, int64_t N, int64_t K) {
     // keep the fp32 partials (written and read once) below the weight bytes
     const int64_t cap = std::max<int64_t>(1, K / (16 * std::max<int64_t>(M, 1)));
     s = std::min<int64_t>(std::min<int64_t>(s, cap), groups);
+    // One workgroup per CU fits the packed 64-row kernel: a second round of workgroups
+    // costs more than a finer K split saves (33..48 rows, QKV + O: 26-28 -> 22-23 us per
+    // layer).  The fp16-weight kernel holds two per CU and keeps the finer split.
+    if (int4 && pl.mt == 64) s = std::max<int64_t>(1, std::min<int64_t>(s, kCus / wgs));
   }
   // every split gets the same whole number of groups
   const int64_t per = (groups + s - 1) / std::max<int64_t>(s, 1);
@@ -995,6 +1025,13 @@ Layout layout(int64_t M, int64_t N, int64_t K, const fi::gemm::Plan& pl, bool in
   return l;
 }
 
+// What the size queries report: the larger of the packed and the fp16 weight forms.
+size_t workspace_bytes_for(int64_t M, int64_t N, int64_t K, bool norm) {
+  using fi::gemm::plan;
+  return std::max(layout(M, N, K, plan(M, N, K, true), true, norm).total,
+                  layout(M, N, K, plan(M, N, K, false), false, norm).total);
+}
+
 // One linear-layer call on any path; norm_w non-null applies RMSNorm to X first.
 int run_linear(const char* fn, const void* x, int64_t x_stride, int64_t M, int64_t K,
                const void* norm_w, float eps, const void* w, int64_t w_stride,
@@ -1004,7 +1041,7 @@ int run_linear(const char* fn, const void* x, int64_t x_stride, int64_t M, int64
   using namespace fi::gemm;
   const bool int4 = scales != nullptr;
   const bool norm = norm_w != nullptr;
-  const Plan pl = plan(M, N, K);
+  const Plan pl = plan(M, N, K, int4);
   const Layout l = layout(M, N, K, pl, int4, norm);
   if (l.total && (!workspace || workspace_bytes < l.total || ((uintptr_t)workspace & 255))) {
     set_error("%s: workspace of %zu bytes (256-byte aligned) needed, %zu given", fn, l.total,
@@ -1066,7 +1103,7 @@ int run_linear(const char* fn, const void* x, int64_t x_stride, int64_t M, int64
 
 extern "C" size_t fi_int4_matmul_workspace_size(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0 || K % fi::gemm::kGroup) return 0;
-  return layout(M, N, K, fi::gemm::plan(M, N, K), true, false).total;  // the larger form
+  return workspace_bytes_for(M, N, K, false);
 }
 
 extern "C" int fi_int4_matmul(const void* x, int64_t x_stride, int64_t M, int64_t K,
@@ -1085,7 +1122,7 @@ extern "C" int fi_int4_matmul(const void* x, int64_t x_stride, int64_t M, int64_
 
 extern "C" size_t fi_rmsnorm_int4_matmul_workspace_size(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0 || K % fi::gemm::kGroup) return 0;
-  return layout(M, N, K, fi::gemm::plan(M, N, K), true, true).total;
+  return workspace_bytes_for(M, N, K, true);
 }
 
 extern "C" int fi_rmsnorm_int4_matmul(const void* x, int64_t x_stride, int64_t M, int64_t K,

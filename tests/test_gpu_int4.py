@@ -95,9 +95,14 @@ def test_int4_matmul_strided_x_and_batch_dims(hip):
 
 # 17..64 rows run the LDS-staged kernel (gemm_dma_kernel): one K group, a two-way K split
 # whose second part is shorter, an 11-way split of 64 groups, partial last column tiles,
-# strided X rows
+# strided X rows, a split capped to one workgroup per CU (48 rows of the QKV shape), an
+# N that is not a multiple of 4 with and without a K split (scalar partial and output
+# stores), and a grid of 257 column tiles with no K split (fp16 output written from the
+# staged tile)
 @pytest.mark.parametrize("M,N,K,pad", [(17, 64, 128, 0), (20, 130, 640, 0), (40, 70, 8192, 264),
-                                       (64, 200, 3072, 512), (33, 5120, 3072, 8)])
+                                       (64, 200, 3072, 512), (33, 5120, 3072, 8),
+                                       (48, 5120, 3072, 0), (36, 130, 3072, 0), (17, 66, 128, 0),
+                                       (50, 16400, 256, 0)])
 def test_int4_matmul_lds_staged_shapes(hip, M, N, K, pad):
     banner(f"int4_matmul staged M={M} N={N} K={K} row pad {pad}")
     from fast_infer_amd import dequantize_int4, int4_matmul, quantize_int4_groupwise
