@@ -298,8 +298,8 @@ FI_API int fi_kv_reset(int32_t* block_table, int64_t bt_stride, int64_t max_bloc
  *   Each weight is fp16(q * scale) exactly as the reference dequantizes it; products are
  *   accumulated in fp32 and rounded to fp16 once.  groupsize must be 128 and K a multiple
  *   of 128.  Some shapes split K: then a workspace of
- *   fi_int4_matmul_workspace_size(M, N, K) bytes is required (FI_ERR_WORKSPACE otherwise);
- *   calls that overlap in time must not share one.
+ *   fi_int4_matmul_workspace_size(M, N, K) bytes (enough for either weight form) is
+ *   required (FI_ERR_WORKSPACE otherwise); calls that overlap in time must not share one.
  */
 FI_API size_t fi_int4_matmul_workspace_size(int64_t M, int64_t N, int64_t K);
 FI_API int fi_int4_matmul(const void* x, int64_t x_stride, int64_t M, int64_t K,
