@@ -17,7 +17,11 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kHeadDim = 128;  // the only head_dim the kernels implement
+// The attention kernels lay out K/V rows, Q and O fragments for 128 columns.  A smaller
+// head_dim (a multiple of 8) runs the same code: the 16-byte chunks past it are loaded as
+// zeros, which add nothing to the dot products, and are never stored.
+constexpr int kHeadDim = 128;
+inline bool head_dim_ok(int64_t d) { return d >= 8 && d <= kHeadDim && d % 8 == 0; }
 constexpr float kLog2e = 1.4426950408889634f;
 // Finite "minus infinity" for running maxima: exp2(x - kNegBig) stays finite and
 // exp2(-inf - kNegBig) == 0, so rows that have seen no valid key produce no NaN.

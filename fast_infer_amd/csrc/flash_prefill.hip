@@ -69,6 +69,8 @@ struct Params {
   const int32_t* block_table;
   int64_t bt_stride;
   int max_blocks_per_seq;
+  int head_dim;      // D <= kHeadDim, a multiple of 8: tiles and fragments stay kHeadDim
+  int d_chunks;      // wide, and the 16-byte chunks past D are loaded as zeros
 };
 
 // LDS tile layouts ("panels"): a K tile is 4 panels of 64 bytes per key (head_dim
@@ -111,7 +113,7 @@ __device__ __forceinline__ void issue_tile_part(const Params& p, __amdgpu_buffer
     const int key = k0 + row0 + (lane >> 2);
     const bool ok = k0 >= 0 && key < p.seq_len;
     const int ch = 4 * panel + ((lane & 3) ^ ((lane >> 4) & 3));
-    const int off = ok ? key * p.k_row_bytes + (ch << 4) : kOutOfRange;
+    const int off = ok && ch < p.d_chunks ? key * p.k_row_bytes + (ch << 4) : kOutOfRange;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
         kr, (lds_void*)(stage + panel * kKPanel + row0 * 64), 16, off, 0, 0, 0);
   }
@@ -119,7 +121,8 @@ __device__ __forceinline__ void issue_tile_part(const Params& p, __amdgpu_buffer
     const int panel = n & 7, row0 = 32 * (n >> 3);
     const int key = k0 + row0 + (lane >> 1);
     const bool ok = k0 >= 0 && key < p.seq_len;
-    const int off = ok ? key * p.v_row_bytes + ((2 * panel + (lane & 1)) << 4) : kOutOfRange;
+    const int ch = 2 * panel + (lane & 1);
+    const int off = ok && ch < p.d_chunks ? key * p.v_row_bytes + (ch << 4) : kOutOfRange;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
         vr, (lds_void*)(stage + kTileBytes + panel * kVPanel + row0 * 32), 16, off, 0, 0, 0);
   }
@@ -145,7 +148,7 @@ __device__ __forceinline__ int64_t pool_block_base(const Params& p, bool row_ok,
   asm volatile("" : "+v"(entry));
   entry = __builtin_amdgcn_readfirstlane(entry);
   if (!row_ok || entry < 0 || entry >= p.num_pool_blocks) return -1;
-  return (int64_t)entry * kPoolBlock * p.num_kv_heads * kHeadDim + (int64_t)kvh * kHeadDim;
+  return (int64_t)entry * kPoolBlock * p.num_kv_heads * p.head_dim + (int64_t)kvh * p.head_dim;
 }
 
 // Copy the resident diagonal tile from LDS into its pool block.
@@ -154,12 +157,12 @@ __device__ __forceinline__ void write_pool(const Params& p, const char* stage, b
                                            int entry, int kvh, int k0, int tid) {
   const int64_t base = pool_block_base(p, row_ok, entry, kvh);
   if (base < 0) return;
-  const int64_t row_stride = (int64_t)p.num_kv_heads * kHeadDim;
+  const int64_t row_stride = (int64_t)p.num_kv_heads * p.head_dim;
 #pragma unroll
   for (int j = 0; j < kKTile * 16 / NT; ++j) {
     const int f = NT * j + tid;
     const int slot = f >> 4;  // row within the tile
-    if (k0 + slot >= p.seq_len) continue;
+    if (k0 + slot >= p.seq_len || (f & 15) >= p.d_chunks) continue;
     const int64_t dst = base + slot * row_stride + 8 * (f & 15);
     *(u32x4*)(p.k_cache + dst) = *(const u32x4*)(stage + k_off(slot, f & 15));
     *(u32x4*)(p.v_cache + dst) = *(const u32x4*)(stage + kTileBytes + v_off(slot, f & 15));
@@ -175,19 +178,19 @@ __device__ __forceinline__ void write_pool_wave(const Params& p, const char* sta
   static_assert(kWaves == 4 && kKTile == 64, "wave split of the pool copy");
   const int64_t base = pool_block_base(p, row_ok, entry, kvh);
   if (base < 0) return;
-  const int64_t row_stride = (int64_t)p.num_kv_heads * kHeadDim;
+  const int64_t row_stride = (int64_t)p.num_kv_heads * p.head_dim;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int f = 64 * j + lane;
     {
       const int slot = 16 * w + (f >> 4), ch = f & 15;
-      if (k0 + slot < p.seq_len)
+      if (k0 + slot < p.seq_len && ch < p.d_chunks)
         *(u32x4*)(p.k_cache + base + slot * row_stride + 8 * ch) =
             *(const u32x4*)(stage + k_off(slot, ch));
     }
     {
       const int slot = 32 * (w >> 1) + (f >> 3), ch = 8 * (w & 1) + (f & 7);
-      if (k0 + slot < p.seq_len)
+      if (k0 + slot < p.seq_len && ch < p.d_chunks)
         *(u32x4*)(p.v_cache + base + slot * row_stride + 8 * ch) =
             *(const u32x4*)(stage + kTileBytes + v_off(slot, ch));
     }
@@ -419,7 +422,7 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(Params p) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       u32x4 v = {0u, 0u, 0u, 0u};
-      if (qpos < p.q_rows) v = *(const u32x4*)(qrow + 32 * i + 8 * g);
+      if (qpos < p.q_rows && 32 * i + 8 * g < p.head_dim) v = *(const u32x4*)(qrow + 32 * i + 8 * g);
       qf[j][i] = as_half8(v ^ p.q_sign);  // exact negation when sm_scale < 0
     }
   }
@@ -511,7 +514,7 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(Params p) {
       const int rl = 4 * rr + r4;
       const u32x4 v = *(const u32x4*)(ostage + (j * kRowsPerWave + rl) * kORow + 16 * c16);
       const int pos = q0 + kRowsPerWave * w + rl;
-      if (pos < p.seq_len)
+      if (pos < p.seq_len && c16 < p.d_chunks)
         *(u32x4*)(p.o + (int64_t)b * p.o_sb + (int64_t)(head0 + j) * p.o_sh +
                   (int64_t)pos * p.o_ss + 8 * c16) = v;
     }
@@ -540,8 +543,8 @@ extern "C" int fi_flash_attention_fwd(const void* q, const void* k, const void* 
   using namespace fi;
   using namespace fi::prefill;
   clear_error();
-  if (head_dim != kHeadDim) {
-    set_error("fi_flash_attention_fwd: head_dim %lld not supported (only %d)",
+  if (!head_dim_ok(head_dim)) {
+    set_error("fi_flash_attention_fwd: head_dim %lld not supported (a multiple of 8 up to %d)",
               (long long)head_dim, kHeadDim);
     return FI_ERR_UNSUPPORTED;
   }
@@ -626,8 +629,10 @@ extern "C" int fi_flash_attention_fwd(const void* q, const void* k, const void* 
   p.block_table = block_table;
   p.bt_stride = bt_stride;
   p.max_blocks_per_seq = (int)max_blocks_per_seq;
-  const int64_t k_span = (seq_len - 1) * k_ss * 2 + kHeadDim * 2;
-  const int64_t v_span = (seq_len - 1) * v_ss * 2 + kHeadDim * 2;
+  p.head_dim = (int)head_dim;
+  p.d_chunks = (int)(head_dim / 8);
+  const int64_t k_span = (seq_len - 1) * k_ss * 2 + head_dim * 2;
+  const int64_t v_span = (seq_len - 1) * v_ss * 2 + head_dim * 2;
   if (k_ss <= 0 || v_ss <= 0 || k_span >= kOutOfRange || v_span >= kOutOfRange) {
     set_error("fi_flash_attention_fwd: one head's K/V rows must span < 2 GiB with positive strides");
     return FI_ERR_UNSUPPORTED;

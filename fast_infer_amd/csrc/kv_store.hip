@@ -22,16 +22,17 @@ struct KvStoreParams {
   int64_t num_tokens;
   int64_t start_pos;
   const int32_t* start_pos_per_seq;
-  int64_t total_chunks;  // batch * num_tokens * num_kv_heads * (kHeadDim / 8)
+  int64_t head_dim;      // a multiple of 8
+  int64_t total_chunks;  // batch * num_tokens * num_kv_heads * (head_dim / 8)
 };
 
 __global__ __launch_bounds__(256) void kv_store_kernel(KvStoreParams p) {
-  constexpr int kChunks = kHeadDim / 8;
+  const int64_t chunks = p.head_dim / 8;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < p.total_chunks;
        idx += stride) {
-    const int chunk = (int)(idx % kChunks);
-    int64_t rest = idx / kChunks;
+    const int64_t chunk = idx % chunks;
+    int64_t rest = idx / chunks;
     const int64_t h = rest % p.num_kv_heads;
     rest /= p.num_kv_heads;
     const int64_t t = rest % p.num_tokens;
@@ -46,7 +47,7 @@ __global__ __launch_bounds__(256) void kv_store_kernel(KvStoreParams p) {
     if (phys < 0 || phys >= p.num_pool_blocks) continue;
 
     const int64_t dst =
-        ((phys * p.block_size + pos % p.block_size) * p.num_kv_heads + h) * kHeadDim + chunk * 8;
+        ((phys * p.block_size + pos % p.block_size) * p.num_kv_heads + h) * p.head_dim + chunk * 8;
     const u32x4 kv = *(const u32x4*)(p.k + b * p.k_sb + t * p.k_st + h * p.k_sh + chunk * 8);
     const u32x4 vv = *(const u32x4*)(p.v + b * p.v_sb + t * p.v_st + h * p.v_sh + chunk * 8);
     *(u32x4*)(p.k_cache + dst) = kv;
@@ -68,9 +69,9 @@ extern "C" int fi_kv_store(const void* k, int64_t k_sb, int64_t k_st, int64_t k_
                            void* stream) {
   using namespace fi;
   clear_error();
-  if (head_dim != kHeadDim) {
-    set_error("fi_kv_store: head_dim %lld not supported (only %d)", (long long)head_dim,
-              kHeadDim);
+  if (head_dim < 8 || head_dim % 8 != 0) {
+    set_error("fi_kv_store: head_dim %lld not supported (a positive multiple of 8)",
+              (long long)head_dim);
     return FI_ERR_UNSUPPORTED;
   }
   if (batch < 0 || num_tokens < 0 || num_kv_heads <= 0 || block_size <= 0 ||
@@ -105,7 +106,8 @@ extern "C" int fi_kv_store(const void* k, int64_t k_sb, int64_t k_st, int64_t k_
   p.num_tokens = num_tokens;
   p.start_pos = start_pos;
   p.start_pos_per_seq = start_pos_per_seq;
-  p.total_chunks = batch * num_tokens * num_kv_heads * (kHeadDim / 8);
+  p.head_dim = head_dim;
+  p.total_chunks = batch * num_tokens * num_kv_heads * (head_dim / 8);
   int64_t blocks = (p.total_chunks + 255) / 256;
   if (blocks > 65536) blocks = 65536;
   hipLaunchKernelGGL(kv_store_kernel, dim3((unsigned)blocks), dim3(256), 0,

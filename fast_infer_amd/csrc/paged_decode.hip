@@ -66,6 +66,8 @@ struct Params {
   float* part_o;   // [batch][num_q_heads][max_splits][128]
   float* part_ml;  // [batch][num_q_heads][max_splits][2]
   int direct;      // 1 -> a single partition, write o
+  int head_dim;    // D <= kHeadDim, a multiple of 8: LDS rows and fragments stay kHeadDim
+  int d_chunks;    // wide, and the 16-byte chunks past D are loaded as zeros
 };
 
 __device__ __forceinline__ int row_context(const Params& p, int b) {
@@ -112,8 +114,8 @@ __device__ __forceinline__ bool issue_tile(const Params& p, const int* s_tab, in
     const bool in = tile + row < split_end;
     const int kc = (lane & 15) ^ row;
     const int vc = (lane & 15) ^ ((row & 7) << 1);
-    const int koff = in ? (slot0 + row) * row_bytes + (kc << 4) : kOutOfRange;
-    const int voff = in ? (slot0 + row) * row_bytes + (vc << 4) : kOutOfRange;
+    const int koff = in && kc < p.d_chunks ? (slot0 + row) * row_bytes + (kc << 4) : kOutOfRange;
+    const int voff = in && vc < p.d_chunks ? (slot0 + row) * row_bytes + (vc << 4) : kOutOfRange;
     lds_copy16_nt(kr, lds + q * 1024, koff, 0);
     lds_copy16_nt(vr, lds + kTileBytes + q * 1024, voff, 0);
   }
@@ -212,9 +214,9 @@ __global__ __launch_bounds__(256, 2) void partition_kernel(Params p) {
 
   __syncthreads();
 
-  const int row_bytes = p.num_kv_heads * kHeadDim * 2;  // one pool slot, all kv heads
+  const int row_bytes = p.num_kv_heads * p.head_dim * 2;  // one pool slot, all kv heads
   const int64_t block_bytes = (int64_t)p.block_size * row_bytes;
-  const int kv_off = kvh * kHeadDim * 2;
+  const int kv_off = kvh * p.head_dim * 2;
   char* wb0 = buf0 + w * kBufBytes;
   char* wb1 = buf1 + w * kBufBytes;
 
@@ -240,7 +242,7 @@ __global__ __launch_bounds__(256, 2) void partition_kernel(Params p) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       u32x4 v = {0u, 0u, 0u, 0u};
-      if (valid) v = *(const u32x4*)(qrow + 32 * i + 8 * g);
+      if (valid && 32 * i + 8 * g < p.head_dim) v = *(const u32x4*)(qrow + 32 * i + 8 * g);
       qf[i] = as_half8(v);
     }
   }
@@ -312,7 +314,8 @@ __global__ __launch_bounds__(256, 2) void partition_kernel(Params p) {
     }
     const int h = head0 + c;
     if (p.direct) {
-      p.o[(int64_t)b * p.o_sb + (int64_t)h * p.o_sh + d] = (half_t)(L > 0.f ? O / L : 0.f);
+      if (d < p.head_dim)
+        p.o[(int64_t)b * p.o_sb + (int64_t)h * p.o_sh + d] = (half_t)(L > 0.f ? O / L : 0.f);
     } else {
       const int64_t slot = ((int64_t)b * p.num_q_heads + h) * p.max_splits + split;
       p.part_o[slot * kHeadDim + d] = O;
@@ -359,7 +362,8 @@ __global__ __launch_bounds__(kHeadDim) void merge_kernel(Params p) {
       mx = mn;
     }
   }
-  p.o[(int64_t)b * p.o_sb + (int64_t)h * p.o_sh + d] = (half_t)(L > 0.f ? O / L : 0.f);
+  if (d < p.head_dim)
+    p.o[(int64_t)b * p.o_sb + (int64_t)h * p.o_sh + d] = (half_t)(L > 0.f ? O / L : 0.f);
 }
 
 // Partition size (tokens, a multiple of kWgTokens) for a call: about kTargetWgs
@@ -401,7 +405,7 @@ extern "C" size_t fi_paged_attention_workspace_size(int64_t batch, int64_t num_q
                                                     int64_t max_num_tokens, int64_t head_dim) {
   using namespace fi::decode;
   if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || max_num_tokens <= 0 ||
-      head_dim != fi::kHeadDim || num_q_heads % num_kv_heads != 0)
+      !fi::head_dim_ok(head_dim) || num_q_heads % num_kv_heads != 0)
     return 0;
   const int64_t group = num_q_heads / num_kv_heads;
   const int64_t wg_per_row = num_kv_heads * (group / heads_per_wg(group));
@@ -424,8 +428,8 @@ int paged_fwd(const char* fn, const void* q, int64_t q_sb, int64_t q_sh, const v
               void* stream) {
   using namespace fi;
   using namespace fi::decode;
-  if (head_dim != kHeadDim) {
-    set_error("%s: head_dim %lld not supported (only %d)", fn,
+  if (!head_dim_ok(head_dim)) {
+    set_error("%s: head_dim %lld not supported (a multiple of 8 up to %d)", fn,
               (long long)head_dim, kHeadDim);
     return FI_ERR_UNSUPPORTED;
   }
@@ -443,7 +447,7 @@ int paged_fwd(const char* fn, const void* q, int64_t q_sb, int64_t q_sh, const v
   }
   if (batch == 0) return FI_OK;
   if (num_tokens > (int64_t)kMaxSplitTokens * kMaxSplits ||
-      block_size * num_kv_heads * kHeadDim * 2 > ((int64_t)1 << 30)) {
+      block_size * num_kv_heads * head_dim * 2 > ((int64_t)1 << 30)) {
     set_error("%s: num_tokens %lld or block bytes too large", fn,
               (long long)num_tokens);
     return FI_ERR_UNSUPPORTED;
@@ -486,6 +490,8 @@ int paged_fwd(const char* fn, const void* q, int64_t q_sb, int64_t q_sh, const v
   if (splits < 1) splits = 1;
   p.max_splits = (int)splits;
   p.direct = splits == 1;
+  p.head_dim = (int)head_dim;
+  p.d_chunks = (int)(head_dim / 8);
   p.part_o = nullptr;
   p.part_ml = nullptr;
   if (!p.direct) {

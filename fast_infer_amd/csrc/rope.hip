@@ -9,11 +9,12 @@
 // Arithmetic is the reference's fp16 tensor arithmetic, op by op (rope.py:37-42):
 //   out = fp16( fp16(x * cos) + fp16(rotate_half(x) * sin) ),
 // each product and the sum formed in fp32 and rounded to fp16 (round-to-nearest-even),
-// rotate_half(x)[i] = -x[i + 64] for i < 64 and x[i - 64] for i >= 64, with cos/sin the
-// reference's fp16 table rows at the token's position.  Results are therefore bit-exact.
+// rotate_half(x)[i] = -x[i + D/2] for i < D/2 and x[i - D/2] for i >= D/2 (D = head_dim,
+// a multiple of 16), with cos/sin the reference's fp16 table rows at the token's position.
+// Results are therefore bit-exact.
 //
-// Work item: one 128-wide head row of one token is 8 lanes; lane c handles elements
-// 8c..8c+7 and their rotation partners 8c+64..8c+71 (16-byte loads and stores).
+// Work item: one head row of one token is D/16 lanes; lane c handles elements 8c..8c+7 and
+// their rotation partners 8c+D/2..8c+D/2+7 (16-byte loads and stores).
 #include "common.h"
 
 namespace fi {
@@ -26,7 +27,7 @@ struct Params {
   int64_t q_sb, q_st, q_sh;
   int64_t k_sb, k_st, k_sh;
   int64_t v_sb, v_st, v_sh;
-  const half_t* cos_t;  // [table_rows, 128]
+  const half_t* cos_t;  // [table_rows, head_dim]
   const half_t* sin_t;
   int table_rows;
   half_t* q_out;
@@ -46,7 +47,10 @@ struct Params {
   int start_pos;
   const int32_t* start_pos_per_seq;
   int heads;      // head rows per token in the grid: q heads, then k heads, then v heads
-  int64_t items;  // batch * num_tokens * heads * 8
+  int head_dim;   // D, a multiple of 16: a row's two halves are D / 16 chunks of 8 each
+  int half;       // D / 2, the rotate-half partner distance
+  int cpr;        // D / 16 work items per row
+  int64_t items;  // batch * num_tokens * heads * cpr
 };
 
 __device__ __forceinline__ half_t rot1(half_t x, half_t c, half_t y, half_t s) {
@@ -66,8 +70,9 @@ __global__ __launch_bounds__(256) void rope_store_kernel(Params p) {
   const Index items = (Index)p.items;
   for (Index it = (Index)blockIdx.x * blockDim.x + threadIdx.x; it < items;
        it += (Index)gridDim.x * blockDim.x) {
-    const int c = (int)(it & 7);
-    const Index row = it >> 3;  // (b, t, head)
+    const Index cpr = (Index)p.cpr;
+    const Index row = it / cpr;  // (b, t, head)
+    const int c = (int)(it - row * cpr);
     const int hh = (int)(row % heads);
     const Index bt = row / heads;
     const int t = (int)(bt % (Index)p.num_tokens);
@@ -83,7 +88,7 @@ __global__ __launch_bounds__(256) void rope_store_kernel(Params p) {
         const int64_t phys = p.block_table[(int64_t)b * p.bt_stride + lb];
         if (phys >= 0 && phys < p.num_pool_blocks) {
           const int hk = hh - p.num_q_heads - (hh >= p.num_q_heads + p.num_kv_heads ? p.num_kv_heads : 0);
-          dst = ((phys * p.block_size + pos % p.block_size) * p.num_kv_heads + hk) * kHeadDim;
+          dst = ((phys * p.block_size + pos % p.block_size) * p.num_kv_heads + hk) * p.head_dim;
         }
       }
     }
@@ -93,7 +98,7 @@ __global__ __launch_bounds__(256) void rope_store_kernel(Params p) {
       const int hk = hh - p.num_q_heads - p.num_kv_heads;
       const half_t* src = p.v + (int64_t)b * p.v_sb + (int64_t)t * p.v_st + (int64_t)hk * p.v_sh;
       *(u32x4*)(p.v_cache + dst + 8 * c) = *(const u32x4*)(src + 8 * c);
-      *(u32x4*)(p.v_cache + dst + 64 + 8 * c) = *(const u32x4*)(src + 64 + 8 * c);
+      *(u32x4*)(p.v_cache + dst + p.half + 8 * c) = *(const u32x4*)(src + p.half + 8 * c);
       continue;
     }
 
@@ -102,33 +107,33 @@ __global__ __launch_bounds__(256) void rope_store_kernel(Params p) {
                              : p.k + (int64_t)b * p.k_sb + (int64_t)t * p.k_st +
                                    (int64_t)(hh - p.num_q_heads) * p.k_sh;
     const half8 lo = as_half8(*(const u32x4*)(src + 8 * c));        // x[8c .. 8c+7]
-    const half8 hi = as_half8(*(const u32x4*)(src + 64 + 8 * c));   // x[64+8c .. 64+8c+7]
-    const half_t* cr = p.cos_t + (int64_t)pos * kHeadDim;
-    const half_t* sr = p.sin_t + (int64_t)pos * kHeadDim;
+    const half8 hi = as_half8(*(const u32x4*)(src + p.half + 8 * c));  // x[D/2+8c .. +7]
+    const half_t* cr = p.cos_t + (int64_t)pos * p.head_dim;
+    const half_t* sr = p.sin_t + (int64_t)pos * p.head_dim;
     const half8 clo = as_half8(*(const u32x4*)(cr + 8 * c));
-    const half8 chi = as_half8(*(const u32x4*)(cr + 64 + 8 * c));
+    const half8 chi = as_half8(*(const u32x4*)(cr + p.half + 8 * c));
     const half8 slo = as_half8(*(const u32x4*)(sr + 8 * c));
-    const half8 shi = as_half8(*(const u32x4*)(sr + 64 + 8 * c));
+    const half8 shi = as_half8(*(const u32x4*)(sr + p.half + 8 * c));
     half8 olo, ohi;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      olo[e] = rot1(lo[e], clo[e], -hi[e], slo[e]);  // i < 64: partner -x[i+64]
-      ohi[e] = rot1(hi[e], chi[e], lo[e], shi[e]);   // i >= 64: partner x[i-64]
+      olo[e] = rot1(lo[e], clo[e], -hi[e], slo[e]);  // i < D/2: partner -x[i+D/2]
+      ohi[e] = rot1(hi[e], chi[e], lo[e], shi[e]);   // i >= D/2: partner x[i-D/2]
     }
     if (is_q) {
       half_t* o = p.q_out + (int64_t)b * p.qo_sb + (int64_t)t * p.qo_st + (int64_t)hh * p.qo_sh;
       *(u32x4*)(o + 8 * c) = as_u32x4(olo);
-      *(u32x4*)(o + 64 + 8 * c) = as_u32x4(ohi);
+      *(u32x4*)(o + p.half + 8 * c) = as_u32x4(ohi);
     } else {
       if (p.k_out) {
         half_t* o = p.k_out + (int64_t)b * p.ko_sb + (int64_t)t * p.ko_st +
                     (int64_t)(hh - p.num_q_heads) * p.ko_sh;
         *(u32x4*)(o + 8 * c) = as_u32x4(olo);
-        *(u32x4*)(o + 64 + 8 * c) = as_u32x4(ohi);
+        *(u32x4*)(o + p.half + 8 * c) = as_u32x4(ohi);
       }
       if (dst >= 0) {
         *(u32x4*)(p.k_cache + dst + 8 * c) = as_u32x4(olo);
-        *(u32x4*)(p.k_cache + dst + 64 + 8 * c) = as_u32x4(ohi);
+        *(u32x4*)(p.k_cache + dst + p.half + 8 * c) = as_u32x4(ohi);
       }
     }
   }
@@ -153,9 +158,9 @@ extern "C" int fi_rope_store_kv(const void* q, int64_t q_sb, int64_t q_st, int64
   using namespace fi;
   using namespace fi::rope;
   clear_error();
-  if (head_dim != kHeadDim) {
-    set_error("fi_rope_store_kv: head_dim %lld not supported (only %d)", (long long)head_dim,
-              kHeadDim);
+  if (head_dim < 16 || head_dim % 16 != 0 || head_dim > (1 << 16)) {
+    set_error("fi_rope_store_kv: head_dim %lld not supported (a positive multiple of 16)",
+              (long long)head_dim);
     return FI_ERR_UNSUPPORTED;
   }
   if (batch < 0 || num_tokens < 0 || num_q_heads < 0 || num_kv_heads < 0 || table_rows < 0) {
@@ -218,7 +223,10 @@ extern "C" int fi_rope_store_kv(const void* q, int64_t q_sb, int64_t q_st, int64
   const int64_t nk = (k_out || pool) ? num_kv_heads : 0;
   const int64_t nv = pool ? num_kv_heads : 0;
   p.heads = (int)(num_q_heads + nk + nv);
-  p.items = batch * num_tokens * p.heads * 8;
+  p.head_dim = (int)head_dim;
+  p.half = (int)(head_dim / 2);
+  p.cpr = (int)(head_dim / 16);
+  p.items = batch * num_tokens * p.heads * p.cpr;
   if (p.items == 0) return FI_OK;
   const int64_t blocks = (p.items + 255) / 256;
   const unsigned grid = (unsigned)(blocks < 65536 ? blocks : 65536);

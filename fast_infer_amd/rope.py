@@ -29,13 +29,16 @@ def precompute_freqs(head_dim: int, max_seq_len: int, theta: float = 500000.0,
     return angles.cos(), angles.sin()
 
 
-def _check_rows(name: str, t: torch.Tensor, heads: int | None = None) -> None:
+def _check_rows(name: str, t: torch.Tensor, heads: int | None = None,
+                head_dim: int | None = None) -> None:
     if t.dtype != torch.float16:
         raise TypeError(f"{name} must be float16, got {t.dtype}")
     if t.device.type != "cuda":
         raise RuntimeError(f"{name} must be on a HIP device; fast_infer_amd has no CPU path")
-    if t.dim() != 4 or t.shape[-1] != 128:
-        raise ValueError(f"{name} must be [batch, tokens, heads, 128], got {tuple(t.shape)}")
+    if t.dim() != 4 or t.shape[-1] % 16 or (head_dim is not None and t.shape[-1] != head_dim):
+        raise ValueError(f"{name} must be [batch, tokens, heads, head_dim] with head_dim a "
+                         f"multiple of 16{'' if head_dim is None else f' ({head_dim})'}, "
+                         f"got {tuple(t.shape)}")
     if heads is not None and t.shape[2] != heads:
         raise ValueError(f"{name} has {t.shape[2]} heads, expected {heads}")
 
@@ -46,9 +49,9 @@ def _rows(t: torch.Tensor) -> torch.Tensor:
     return t
 
 
-def _table(name: str, t: torch.Tensor, device) -> torch.Tensor:
-    if t.dim() != 2 or t.shape[1] != 128:
-        raise ValueError(f"{name} must be [rows, 128], got {tuple(t.shape)}")
+def _table(name: str, t: torch.Tensor, device, head_dim: int) -> torch.Tensor:
+    if t.dim() != 2 or t.shape[1] != head_dim:
+        raise ValueError(f"{name} must be [rows, {head_dim}], got {tuple(t.shape)}")
     if t.dtype != torch.float16 or t.device != device:
         t = t.to(device=device, dtype=torch.float16)
     return t if t.is_contiguous() and t.data_ptr() % 16 == 0 else t.contiguous()
@@ -61,9 +64,9 @@ def rope_store_kv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor | None,
                   start_positions: torch.Tensor | None = None, return_k: bool = True,
                   q_out: torch.Tensor | None = None
                   ) -> tuple[torch.Tensor, torch.Tensor | None]:
-    """Rotate q ``[B, T, Hq, 128]`` and k ``[B, T, Hkv, 128]`` at table rows
-    ``start + t`` (``start`` = ``start_positions[b]`` if given, else ``start_pos``), with
-    fp16 tables ``cos_table`` / ``sin_table`` ``[rows, 128]`` (fp32 tables are converted
+    """Rotate q ``[B, T, Hq, D]`` and k ``[B, T, Hkv, D]`` (D a multiple of 16, 128 in the
+    model) at table rows ``start + t`` (``start`` = ``start_positions[b]`` if given, else
+    ``start_pos``), with fp16 tables ``cos_table`` / ``sin_table`` ``[rows, D]`` (fp32 tables are converted
     on every call; pass fp16 ones on the hot path).  With a pool, rotated k and v also go
     to ``block_table[b, pos // bs]``, slot ``pos % bs`` (block-table entries past the
     table or outside the pool are skipped).  Positions outside the table are an error for
@@ -71,8 +74,8 @@ def rope_store_kv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor | None,
     ``start_positions`` such tokens are skipped on the device, their q/k rows left
     unwritten.  Returns (q_rot, k_rot or None)."""
     _check_rows("q", q)
-    batch, tokens, num_q_heads, _ = q.shape
-    _check_rows("k", k)
+    batch, tokens, num_q_heads, head_dim = q.shape
+    _check_rows("k", k, head_dim=head_dim)
     num_kv_heads = k.shape[2]
     if k.shape[:2] != q.shape[:2]:
         raise ValueError(f"k {tuple(k.shape)} does not match q {tuple(q.shape)}")
@@ -80,14 +83,14 @@ def rope_store_kv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor | None,
     if pool:
         if v is None or v_cache is None or block_table is None:
             raise ValueError("the pool write needs v, v_cache and block_table")
-        _check_rows("v", v, num_kv_heads)
+        _check_rows("v", v, num_kv_heads, head_dim)
         if v.shape[:2] != q.shape[:2]:
             raise ValueError(f"v {tuple(v.shape)} does not match q {tuple(q.shape)}")
         for name, t in (("k_cache", k_cache), ("v_cache", v_cache)):
             if t.dtype != torch.float16 or t.device.type != "cuda":
                 raise TypeError(f"{name} must be a float16 HIP tensor")
         if (k_cache.dim() != 4 or v_cache.shape != k_cache.shape
-                or k_cache.shape[2] != num_kv_heads or k_cache.shape[3] != 128):
+                or k_cache.shape[2] != num_kv_heads or k_cache.shape[3] != head_dim):
             raise ValueError(f"pool {tuple(k_cache.shape)} does not match k {tuple(k.shape)}")
         if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
             raise ValueError("pools must be contiguous")
@@ -97,8 +100,8 @@ def rope_store_kv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor | None,
             raise ValueError("block_table has fewer rows than the batch")
         if block_table.stride(-1) != 1:
             block_table = block_table.contiguous()
-    cos_t = _table("cos_table", cos_table, q.device)
-    sin_t = _table("sin_table", sin_table, q.device)
+    cos_t = _table("cos_table", cos_table, q.device, head_dim)
+    sin_t = _table("sin_table", sin_table, q.device, head_dim)
     if cos_t.shape != sin_t.shape:
         raise ValueError("cos and sin tables differ in shape")
     if start_positions is not None:
@@ -131,7 +134,7 @@ def rope_store_kv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor | None,
         k_cache.shape[0] if pool else 0, k_cache.shape[1] if pool else 0,
         block_table.data_ptr() if pool else None,
         block_table.stride(0) if pool else 0, block_table.shape[1] if pool else 0,
-        batch, tokens, num_q_heads, num_kv_heads, 128,
+        batch, tokens, num_q_heads, num_kv_heads, head_dim,
         int(start_pos), None if start_positions is None else start_positions.data_ptr(),
         _lib.stream_handle(q.device))
     _lib.check(rc, "rope_store_kv")
@@ -140,8 +143,8 @@ def rope_store_kv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor | None,
 
 def apply_rope(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor,
                sin: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """kernels/rope.py:26-44: q ``[B, S, Hq, 128]``, k ``[B, S, Hkv, 128]`` fp16 (strided
-    views fine), cos/sin ``[S, 128]`` fp16 (the table rows of the S positions).
+    """kernels/rope.py:26-44: q ``[B, S, Hq, D]``, k ``[B, S, Hkv, D]`` fp16 (strided
+    views fine), cos/sin ``[S, D]`` fp16 (the table rows of the S positions).
     Returns rotated (q, k), bit-exact with the reference."""
     if cos.dim() != 2 or cos.shape[0] != q.shape[1]:
         raise ValueError(f"cos must be [seq_len, head_dim] for seq_len {q.shape[1]}")
@@ -165,8 +168,8 @@ def rope_store_kv_decode(kv_cache, layer_idx: int, q: torch.Tensor, k: torch.Ten
                          v: torch.Tensor, cos_table: torch.Tensor, sin_table: torch.Tensor,
                          token_pos: int) -> torch.Tensor:
     """model.py:101 + :120 (:185-201) in one pass for one token per row at position
-    ``token_pos``: q ``[B, Hq, 128]``, k/v ``[B, Hkv, 128]``.  At layer 0 increments
-    ``num_tokens``; allocates lazily; returns q_rot ``[B, Hq, 128]``."""
+    ``token_pos``: q ``[B, Hq, D]``, k/v ``[B, Hkv, D]``.  At layer 0 increments
+    ``num_tokens``; allocates lazily; returns q_rot ``[B, Hq, D]``."""
     batch_size = q.shape[0]
     if layer_idx == 0:
         kv_cache.num_tokens += 1

@@ -42,8 +42,10 @@
  *     the process ends.
  *   - Return value: FI_OK or an FI_ERR_* code; fi_last_error() then gives a
  *     message for the calling thread.
- *   - Only head_dim == 128 and fp16 data are implemented (the shapes of
- *     Llama-3.2-3B, config.py:12-15).  Other head dims return
+ *   - fp16 data.  head_dim: a multiple of 8 up to 128 for the attention entry points
+ *     (128 for Llama-3.2-3B, config.py:12-15; the kernels load the columns past a
+ *     smaller head_dim as zeros and never store them), a multiple of 8 for
+ *     fi_kv_store, a multiple of 16 for fi_rope_store_kv.  Other head dims return
  *     FI_ERR_UNSUPPORTED.
  */
 #ifndef FAST_INFER_AMD_H

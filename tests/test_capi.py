@@ -60,18 +60,23 @@ def test_version_and_empty_error(lib):
 
 
 def test_unsupported_head_dim(lib):
+    """head_dim must be a multiple of 8 up to 128 for the attention kernels (a multiple of
+    8 for the KV scatter, of 16 for RoPE); the check comes before any other."""
     from fast_infer_amd import _lib
 
-    rc = lib.fi_paged_attention_fwd(8, 0, 0, 16, 16, 1, 64, 1, 16, 1, 1, None, 1, 32, 0, 0,
-                                    1, 1, 64, 1.0, None, 0, None)
-    assert rc == _lib.FI_ERR_UNSUPPORTED
-    assert b"head_dim 64" in lib.fi_last_error()
-    rc = lib.fi_flash_attention_fwd(16, 16, 16, 16, 1, 1, 1, 1, 96, *([8] * 12), 1.0,
-                                    None, None, 0, 64, None, 0, 0, None)
-    assert rc == _lib.FI_ERR_UNSUPPORTED
-    rc = lib.fi_kv_store(16, 8, 8, 8, 16, 8, 8, 8, 16, 16, 1, 64, 1, 80, 16, 1, 1, 1, 1, 0,
+    for d in (60, 136):
+        rc = lib.fi_paged_attention_fwd(8, 0, 0, 16, 16, 1, 64, 1, 16, 1, 1, None, 1, 32, 0, 0,
+                                        1, 1, d, 1.0, None, 0, None)
+        assert rc == _lib.FI_ERR_UNSUPPORTED
+        assert f"head_dim {d}".encode() in lib.fi_last_error()
+        rc = lib.fi_flash_attention_fwd(16, 16, 16, 16, 1, 1, 1, 1, d, *([8] * 12), 1.0,
+                                        None, None, 0, 64, None, 0, 0, None)
+        assert rc == _lib.FI_ERR_UNSUPPORTED
+        assert lib.fi_paged_attention_workspace_size(4, 8, 8, 4096, d) == 0
+    rc = lib.fi_kv_store(16, 8, 8, 8, 16, 8, 8, 8, 16, 16, 1, 64, 1, 12, 16, 1, 1, 1, 1, 0,
                          None, None)
     assert rc == _lib.FI_ERR_UNSUPPORTED
+    assert lib.fi_paged_attention_workspace_size(4, 8, 8, 4096, 64) > 0
 
 
 def test_invalid_arguments(lib):
@@ -122,8 +127,8 @@ def _rope_args(**kw):
 def test_rope_store_kv_validation(lib):
     from fast_infer_amd import _lib
 
-    assert lib.fi_rope_store_kv(*_rope_args(head_dim=64)) == _lib.FI_ERR_UNSUPPORTED
-    assert b"head_dim 64" in lib.fi_last_error()
+    assert lib.fi_rope_store_kv(*_rope_args(head_dim=72)) == _lib.FI_ERR_UNSUPPORTED
+    assert b"head_dim 72" in lib.fi_last_error()
     assert lib.fi_rope_store_kv(*_rope_args(q=18)) == _lib.FI_ERR_INVALID
     assert b"aligned" in lib.fi_last_error()
     assert lib.fi_rope_store_kv(*_rope_args(k_st=12)) == _lib.FI_ERR_INVALID
@@ -212,7 +217,9 @@ def test_workspace_size(lib):
     assert lib.fi_paged_attention_workspace_size(1, 24, 8, 256, 128) == 0
     n = lib.fi_paged_attention_workspace_size(32, 24, 8, 4096, 128)
     assert n > 0 and n % (32 * 24 * 130 * 4) == 0
-    assert lib.fi_paged_attention_workspace_size(32, 24, 8, 4096, 64) == 0
+    # partials stay 128 columns wide for any supported head_dim; unsupported ones need none
+    assert lib.fi_paged_attention_workspace_size(32, 24, 8, 4096, 64) == n
+    assert lib.fi_paged_attention_workspace_size(32, 24, 8, 4096, 136) == 0
     rc = lib.fi_paged_attention_fwd(16, 3072, 128, 16, 16, 2048, 64, 8, 16, 64, 64, None,
                                     4096, 32, 3072, 128, 32, 24, 128, 1.0, None, 0, None)
     from fast_infer_amd import _lib
