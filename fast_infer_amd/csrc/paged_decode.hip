@@ -17,6 +17,11 @@
 //     O^T = V^T * P^T (v_mfma_f32_16x16x16_f16, V^T fragments from the LDS transpose
 //     read ds_read_b64_tr_b16, P^T straight from the S^T accumulator lanes).
 //   * Online softmax is fp32 in log2 units (exp2 with sm_scale * log2(e) folded in).
+//   * Tiles are laid over token positions, never over blocks, so the block size only
+//     decides where a tile row's bytes come from: with a multiple of 16 a tile sits in one
+//     block (one descriptor per tile); any other size gives each row its own block, through
+//     per-lane offsets into a descriptor over the whole pool (pools under 4 GiB) or through
+//     one descriptor per row.
 #include <mutex>
 
 #include "common.h"
@@ -33,6 +38,15 @@ constexpr int kBufBytes = 2 * kTileBytes;          // K + V tile of one wave
 constexpr int kMaxHeadsPerWg = 16;                 // MFMA N dimension
 constexpr int kMaxSplitTokens = 4096;                       // cap on the partition size
 constexpr int kMaxSplitEntries = kMaxSplitTokens / 16 + 1;  // table entries of a partition
+// Table entries a partition may stage when block_size is not a multiple of 16 (up to
+// tokens_per_split / block_size + 2 of them): 14 KiB, which keeps two workgroups per CU.
+constexpr int kAnyBlockEntries = 3584;
+// How a tile's K/V rows are addressed (the partition kernel's template argument):
+constexpr int kTileBlock = 0;  // block_size % 16 == 0: a 16-token tile lies in one block
+constexpr int kLanePool = 1;   // any block_size, pool under kFarOffset bytes: per-lane offsets
+constexpr int kRowBlock = 2;   // any block_size, any pool: one descriptor per tile row
+// Buffer offset past the end of any pool the kLanePool path serves: loads return 0.
+constexpr uint32_t kFarOffset = 0xFFFFFF00u;
 constexpr int kMaxSplits = 1024;                            // partitions per row
 constexpr int kOutOfRange = 0x40000000;  // buffer offset beyond any block: loads return 0
 // The K/V loads use the non-temporal cache policy (lds_copy16_nt): each byte is read once per
@@ -121,10 +135,93 @@ __device__ __forceinline__ bool issue_tile(const Params& p, const int* s_tab, in
   }
   return phys >= 0;
 }
-constexpr int kIssuePerTile = 8;  // load instructions per issue_tile
+
+// issue_tile for a block_size that is not a multiple of 16 and a pool of fewer than
+// kFarOffset bytes: the 16 rows of a tile may lie in up to 16 pool blocks, so the
+// descriptors kr / vr span the whole pool (from this kv head's first column) and each lane
+// adds its row's block and slot to its own offset; the copies stay four 4-row copies per
+// tile.  Returns the tile's row mask: bit r is set when token tile + r is before split_end
+// and its table entry is inside the pool.
+__device__ __forceinline__ uint32_t issue_tile_lanes(const Params& p, const int* s_tab, int tab0,
+                                                     int tile, int split_end, rsrc_t kr,
+                                                     rsrc_t vr, uint32_t block_bytes,
+                                                     int row_bytes, char* buf, int lane) {
+  const uint32_t lds = lds_addr(buf);
+  const int grp = lane >> 4;
+  uint32_t rows = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int row = 4 * q + grp;
+    const int tok = tile + row;
+    const bool in = tok < split_end;
+    const int blk = tok / p.block_size;
+    const int slot = tok - blk * p.block_size;
+    // entries tab0 .. (split_end - 1) / block_size are staged; rows past split_end read none
+    const int phys = in ? s_tab[blk - tab0] : -1;
+    const bool valid = phys >= 0;
+    // lanes 0, 16, 32, 48 hold rows 4q .. 4q + 3
+    const uint64_t m = __builtin_amdgcn_ballot_w64(valid);
+    rows |= (uint32_t)((m & 1u) | ((m >> 15) & 2u) | ((m >> 30) & 4u) | ((m >> 45) & 8u)) << (4 * q);
+    // phys < num_pool_blocks, so the row's offset is below the pool size (< 2^32)
+    const uint32_t at = (uint32_t)phys * block_bytes + (uint32_t)(slot * row_bytes);
+    const int kc = (lane & 15) ^ row;
+    const int vc = (lane & 15) ^ ((row & 7) << 1);
+    const uint32_t koff = valid && kc < p.d_chunks ? at + (uint32_t)(kc << 4) : kFarOffset;
+    const uint32_t voff = valid && vc < p.d_chunks ? at + (uint32_t)(vc << 4) : kFarOffset;
+    lds_copy16_nt(kr, lds + q * 1024, (int)koff, 0);
+    lds_copy16_nt(vr, lds + kTileBytes + q * 1024, (int)voff, 0);
+  }
+  return rows;
+}
+
+// issue_tile for a block_size that is not a multiple of 16 and a pool of any size: every
+// row gets its own descriptor (as in issue_tile), and each of the four 4-row copies becomes
+// four copies with one 16-lane row group active (lane l still fills slot l % 16 of row
+// 4q + l / 16).  Returns the row mask as issue_tile_lanes does.
+__device__ __forceinline__ uint32_t issue_tile_rows(const Params& p, const int* s_tab, int tab0,
+                                                    int tile, int split_end, int kv_off,
+                                                    int64_t block_bytes, int row_bytes,
+                                                    char* buf, int lane) {
+  const uint32_t lds = lds_addr(buf);
+  const int grp = lane >> 4;
+  uint32_t rows = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int row = 4 * q + grp;
+    const int tok = tile + row;
+    const bool in = tok < split_end;
+    const int blk = tok / p.block_size;
+    const int slot = tok - blk * p.block_size;
+    // entries tab0 .. (split_end - 1) / block_size are staged; rows past split_end read none
+    const int phys_lane = in ? s_tab[blk - tab0] : -1;
+    const int kc = (lane & 15) ^ row;
+    const int vc = (lane & 15) ^ ((row & 7) << 1);
+    const int koff = kc < p.d_chunks ? slot * row_bytes + (kc << 4) : kOutOfRange;
+    const int voff = vc < p.d_chunks ? slot * row_bytes + (vc << 4) : kOutOfRange;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int phys = __builtin_amdgcn_readlane(phys_lane, 16 * j);  // row 4q + j
+      rows |= (phys >= 0 ? 1u : 0u) << (4 * q + j);
+      const rsrc_t kr = block_rsrc(p.k_cache, phys, block_bytes, kv_off);
+      const rsrc_t vr = block_rsrc(p.v_cache, phys, block_bytes, kv_off);
+      if (grp == j) {
+        lds_copy16_nt(kr, lds + q * 1024, koff, 0);
+        lds_copy16_nt(vr, lds + kTileBytes + q * 1024, voff, 0);
+      }
+    }
+  }
+  return rows;
+}
+
+// Load instructions one tile issue leaves outstanding per wave.
+template <int kAddr>
+constexpr int kIssuePerTile = kAddr == kRowBlock ? 32 : 8;
 
 // Online-softmax update with one resident 16-token tile at `tile`.
-__device__ __forceinline__ void consume_tile(const Params& p, const char* buf, bool ok, int tile,
+// `rows`: the tile's row mask for kLanePool / kRowBlock; for kTileBlock, nonzero when the
+// tile's block is inside the pool.
+template <int kAddr>
+__device__ __forceinline__ void consume_tile(const Params& p, const char* buf, uint32_t rows, int tile,
                                              int split_end, const half8 (&qf)[4], int col,
                                              int g, float& m_run, float& l_run,
                                              floatx4 (&acc)[8]) {
@@ -140,7 +237,9 @@ __device__ __forceinline__ void consume_tile(const Params& p, const char* buf, b
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int tok = tile + 4 * g + r;
-    x[r] = (ok && tok < split_end) ? s[r] * p.scale_log2 : -__builtin_inff();
+    const bool valid = kAddr == kTileBlock ? rows != 0 && tok < split_end
+                                           : ((rows >> (4 * g + r)) & 1u) != 0;
+    x[r] = valid ? s[r] * p.scale_log2 : -__builtin_inff();
     tmax = fmaxf(tmax, x[r]);
   }
   tmax = row4_max(tmax);
@@ -171,13 +270,14 @@ __device__ __forceinline__ void consume_tile(const Params& p, const char* buf, b
   }
 }
 
+template <int kAddr>
 __global__ __launch_bounds__(256, 2) void partition_kernel(Params p) {
   // two tile buffers per wave (distinct objects, so the compiler tracks the copies into
   // one separately from reads of the other)
   __shared__ __attribute__((aligned(16))) char buf0[kWaves * kBufBytes];
   __shared__ __attribute__((aligned(16))) char buf1[kWaves * kBufBytes];
   __shared__ float s_ml[kWaves * kMaxHeadsPerWg * 2];
-  __shared__ int s_tab[kMaxSplitEntries];
+  __shared__ int s_tab[kAddr == kTileBlock ? kMaxSplitEntries : kAnyBlockEntries];
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave index (uniform)
@@ -225,12 +325,25 @@ __global__ __launch_bounds__(256, 2) void partition_kernel(Params p) {
   // as soon as its tile is consumed.  The first two copies go out before the Q loads.
   const int first = split_start + w * kTileTokens;
   const int n_t = first < split_end ? (split_end - first + kWgTokens - 1) / kWgTokens : 0;
-  bool ok0 = false, ok1 = false;
-  if (n_t > 0)
-    ok0 = issue_tile(p, s_tab, tab0, first, split_end, kv_off, block_bytes, row_bytes, wb0, lane);
-  if (n_t > 1)
-    ok1 = issue_tile(p, s_tab, tab0, first + kWgTokens, split_end, kv_off, block_bytes,
-                     row_bytes, wb1, lane);
+  // kLanePool: descriptors over the whole pools from this kv head's first column (the host
+  // checked that the pool is smaller than kFarOffset bytes)
+  const uint32_t pool_records =
+      p.num_pool_blocks > 0 ? (uint32_t)(p.num_pool_blocks * block_bytes - kv_off) : 0u;
+  const rsrc_t pool_k = raw_rsrc((const char*)p.k_cache + kv_off, (int)pool_records);
+  const rsrc_t pool_v = raw_rsrc((const char*)p.v_cache + kv_off, (int)pool_records);
+  auto issue = [&](int tile, char* wb) -> uint32_t {
+    if (kAddr == kLanePool)
+      return issue_tile_lanes(p, s_tab, tab0, tile, split_end, pool_k, pool_v,
+                              (uint32_t)block_bytes, row_bytes, wb, lane);
+    if (kAddr == kRowBlock)
+      return issue_tile_rows(p, s_tab, tab0, tile, split_end, kv_off, block_bytes, row_bytes, wb,
+                             lane);
+    return issue_tile(p, s_tab, tab0, tile, split_end, kv_off, block_bytes, row_bytes, wb, lane)
+               ? 1u : 0u;
+  };
+  uint32_t ok0 = 0, ok1 = 0;
+  if (n_t > 0) ok0 = issue(first, wb0);
+  if (n_t > 1) ok1 = issue(first + kWgTokens, wb1);
 
   // Q^T fragments (B operand of S^T = K * Q^T): column `col` is query head head0+col;
   // MFMA i takes head_dim d = 32*i + 8*g + s in reduction slot 8*g + s (the K
@@ -260,21 +373,19 @@ __global__ __launch_bounds__(256, 2) void partition_kernel(Params p) {
 
   for (int k = 0; k < n_t; k += 2) {
     const int t0 = first + k * kWgTokens;
-    consume_tile(p, wb0, ok0, t0, split_end, qf, col, g, m_run, l_run, acc);
+    consume_tile<kAddr>(p, wb0, ok0, t0, split_end, qf, col, g, m_run, l_run, acc);
     if (k + 1 >= n_t) break;
     if (k + 2 < n_t) {
-      ok0 = issue_tile(p, s_tab, tab0, t0 + 2 * kWgTokens, split_end, kv_off, block_bytes,
-                       row_bytes, wb0, lane);
-      wait_vmcnt<kIssuePerTile>();
+      ok0 = issue(t0 + 2 * kWgTokens, wb0);
+      wait_vmcnt<kIssuePerTile<kAddr>>();
     } else {
       wait_vmcnt<0>();
     }
-    consume_tile(p, wb1, ok1, t0 + kWgTokens, split_end, qf, col, g, m_run, l_run, acc);
+    consume_tile<kAddr>(p, wb1, ok1, t0 + kWgTokens, split_end, qf, col, g, m_run, l_run, acc);
     if (k + 2 >= n_t) break;
     if (k + 3 < n_t) {
-      ok1 = issue_tile(p, s_tab, tab0, t0 + 3 * kWgTokens, split_end, kv_off, block_bytes,
-                       row_bytes, wb1, lane);
-      wait_vmcnt<kIssuePerTile>();
+      ok1 = issue(t0 + 3 * kWgTokens, wb1);
+      wait_vmcnt<kIssuePerTile<kAddr>>();
     } else {
       wait_vmcnt<0>();
     }
@@ -440,10 +551,9 @@ int paged_fwd(const char* fn, const void* q, int64_t q_sb, int64_t q_sh, const v
               (long long)num_tokens);
     return FI_ERR_INVALID;
   }
-  if (block_size <= 0 || block_size % 16 != 0) {
-    set_error("%s: block_size %lld must be a positive multiple of 16", fn,
-              (long long)block_size);
-    return FI_ERR_UNSUPPORTED;
+  if (block_size <= 0) {
+    set_error("%s: block_size %lld must be positive", fn, (long long)block_size);
+    return FI_ERR_INVALID;
   }
   if (batch == 0) return FI_OK;
   if (num_tokens > (int64_t)kMaxSplitTokens * kMaxSplits ||
@@ -492,6 +602,18 @@ int paged_fwd(const char* fn, const void* q, int64_t q_sb, int64_t q_sh, const v
   p.direct = splits == 1;
   p.head_dim = (int)head_dim;
   p.d_chunks = (int)(head_dim / 8);
+  // A partition stages the table entries of its tokens in LDS: at most
+  // (tokens_per_split - 1) / block_size + 2 of them (always within kMaxSplitEntries for a
+  // multiple of 16).
+  const int64_t block_bytes = block_size * num_kv_heads * head_dim * 2;  // <= 1 GiB here
+  const int addr = block_size % 16 == 0 ? kTileBlock
+                   : num_pool_blocks <= ((int64_t)kFarOffset - 1) / block_bytes ? kLanePool
+                                                                                : kRowBlock;
+  if (addr != kTileBlock && (p.tokens_per_split - 1) / block_size + 2 > kAnyBlockEntries) {
+    set_error("%s: num_tokens %lld too large for block_size %lld", fn, (long long)num_tokens,
+              (long long)block_size);
+    return FI_ERR_UNSUPPORTED;
+  }
   p.part_o = nullptr;
   p.part_ml = nullptr;
   if (!p.direct) {
@@ -510,7 +632,13 @@ int paged_fwd(const char* fn, const void* q, int64_t q_sb, int64_t q_sh, const v
     return FI_ERR_UNSUPPORTED;
   }
   const dim3 grid((unsigned)wg_per_row, (unsigned)splits, (unsigned)batch);
-  hipLaunchKernelGGL(partition_kernel, grid, dim3(kWaves * 64), 0, (hipStream_t)stream, p);
+  const dim3 block(kWaves * 64);
+  if (addr == kTileBlock)
+    hipLaunchKernelGGL(partition_kernel<kTileBlock>, grid, block, 0, (hipStream_t)stream, p);
+  else if (addr == kLanePool)
+    hipLaunchKernelGGL(partition_kernel<kLanePool>, grid, block, 0, (hipStream_t)stream, p);
+  else
+    hipLaunchKernelGGL(partition_kernel<kRowBlock>, grid, block, 0, (hipStream_t)stream, p);
   int rc = check_launch(fn);
   if (rc != FI_OK || p.direct) return rc;
   hipLaunchKernelGGL(merge_kernel, dim3((unsigned)num_q_heads, (unsigned)batch), dim3(kHeadDim), 0,

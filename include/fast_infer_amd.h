@@ -129,7 +129,9 @@ FI_API size_t fi_paged_attention_workspace_size(int64_t batch, int64_t num_q_hea
  *                 else int32[batch] per-row lengths, each clamped to num_tokens, so
  *                 num_tokens must be >= max(context_lens).
  *   Rows whose length is 0 produce zeros (kernels/attention.py:205-206).
- *   block_size must be a multiple of 16.  workspace must hold
+ *   Any block_size >= 1 (a multiple of 16 keeps every 16-token tile inside one block; other
+ *   sizes address each tile row through its own block at about the same speed); with
+ *   block_size 1 a call takes at most 3520 * 1024 tokens.  workspace must hold
  *   fi_paged_attention_workspace_size(batch, num_q_heads, num_kv_heads, num_tokens, head_dim)
  *   bytes (it may be NULL when that is 0); its contents need no initialisation.
  */

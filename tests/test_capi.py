@@ -94,10 +94,14 @@ def test_invalid_arguments(lib):
     rc = lib.fi_flash_attention_fwd(16, 16, 16, 16, 1, 8, 8, 8, 128, *([8] * 12), 1.0,
                                     32, 32, 4, 32, 64, 4, 4, None)
     assert rc == _lib.FI_ERR_UNSUPPORTED
-    # block size not a multiple of 16 for decode
-    rc = lib.fi_paged_attention_fwd(16, 8, 8, 16, 16, 1, 24, 1, 16, 1, 1, None, 1, 32, 8, 8,
+    # decode block size 0
+    rc = lib.fi_paged_attention_fwd(16, 8, 8, 16, 16, 1, 0, 1, 16, 1, 1, None, 1, 32, 8, 8,
                                     1, 1, 128, 1.0, None, 0, None)
-    assert rc == _lib.FI_ERR_UNSUPPORTED
+    assert rc == _lib.FI_ERR_INVALID
+    # block size 1 with partitions whose table entries would not fit the staging area
+    rc = lib.fi_paged_attention_fwd(16, 8, 8, 16, 16, 1, 1, 1, 16, 1, 1, None, 4_000_000, 32,
+                                    8, 8, 1, 1, 128, 1.0, None, 0, None)
+    assert rc == _lib.FI_ERR_UNSUPPORTED and b"block_size 1" in lib.fi_last_error()
     # null pools
     rc = lib.fi_kv_store(16, 8, 8, 8, 16, 8, 8, 8, None, None, 1, 64, 1, 128, 16, 1, 1, 1, 1,
                          0, None, None)
