@@ -168,3 +168,37 @@ def test_paged_decode_block_size_pool_over_4gib(hip):
     assert torch.equal(big, small)
     ref = OA.paged_attention(q.cpu(), kc.cpu(), vc.cpu(), table, bs, lens)
     assert _maxabs(small, ref) <= ATOL
+
+
+@pytest.mark.parametrize("bs", [8, 1])
+def test_paged_decode_block_size_graph_replay(hip, bs):
+    # captured once, replayed with other decode calls and synchronisation between replays;
+    # each replay equals the eager call bit for bit (the kernels record no memset)
+    banner(f"paged decode block_size {bs}, HIP graph replay")
+    from fast_infer_amd import paged_attention, paged_attention_workspace
+
+    lens = [900, 3000, 17, 2048]
+    q, kc, vc, table, lens = _inputs(bs, lens, Hq=24, Hkv=8, seed=20 + bs)
+    q, kc, vc, table = q.to(DEV), kc.to(DEV), vc.to(DEV), table.to(DEV)
+    cl = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    ws = paged_attention_workspace(len(lens), 24, 8, 3000, 128, DEV)
+    ref = paged_attention(q, kc, vc, table, bs, 3000, context_lens=cl, workspace=ws).clone()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        paged_attention(q, kc, vc, table, bs, 3000, context_lens=cl, workspace=ws)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = paged_attention(q, kc, vc, table, bs, 3000, context_lens=cl, workspace=ws)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        paged_attention(torch.randn_like(q), kc, vc, table, bs, 3000, context_lens=cl,
+                        workspace=ws)
+        torch.cuda.synchronize()
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), rep
