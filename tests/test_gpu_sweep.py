@@ -1,6 +1,7 @@
 """Seeded sweeps of random valid configurations against the oracle (marked ``gpu``).
 
-* paged decode: block sizes 16..128, GQA groups 1..8 (and 32 query heads per kv head),
+* paged decode: block sizes 16..128 (seeds 0..11) and 1..100 off the 16-token tile grid
+  (seeds 12..19), GQA groups 1..8 (and 32 query heads per kv head),
   1..12 ragged rows including empty ones, shuffled tables wider than needed with -1
   padding, sm_scale of either sign;
 * causal prefill: GQA groups 1..8 (every heads-per-workgroup instantiation), lengths
@@ -38,13 +39,14 @@ DECODE_HEADS = [(24, 8), (8, 8), (16, 8), (32, 8), (12, 4), (6, 2), (64, 8), (10
                 (64, 2), (40, 8), (3, 1)]
 
 
-@pytest.mark.parametrize("seed", range(12))
+@pytest.mark.parametrize("seed", range(20))
 def test_paged_decode_random(hip, seed):
     from fast_infer_amd import paged_attention
 
     rng = np.random.default_rng(1000 + seed)
-    Hq, Hkv = DECODE_HEADS[seed]
-    bs = int(rng.choice([16, 32, 64, 128]))
+    Hq, Hkv = DECODE_HEADS[seed % len(DECODE_HEADS)]
+    sizes = [16, 32, 64, 128] if seed < 12 else [1, 2, 4, 8, 12, 24, 40, 100]
+    bs = int(rng.choice(sizes))
     B = int(rng.integers(1, 13))
     lens = [int(x) for x in rng.integers(0, 900, B)]
     if B > 2:
