@@ -1,8 +1,8 @@
 """CPU oracle for the attention hot path and its RoPE producer — TEST INFRASTRUCTURE, never a product path.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may
-import, call, link or execute anything in this package, and only as the checker (or
-the timed CPU baseline) — the ``fast_infer_amd`` package never does.
+import, call, link or execute anything in this package, and only to check results against
+(or as the timed CPU baseline) — the ``fast_infer_amd`` package never does.
 
 Contents (each function cites the reference file:line it restates):
 
