@@ -209,10 +209,13 @@ __device__ __forceinline__ u32x2 vt_read(const char* vs, int row0, int dt, int c
 }
 
 // PV of half c of a resident tile: O^T += V^T P^T (slots 0..3 = keys 4g..4g+3,
-// 4..7 = 16+4g..16+4g+3).
+// 4..7 = 16+4g..16+4g+3) in tiles 0..7, and the softmax denominator l in tile 8: an
+// all-ones A operand puts sum_k p[k][q] (the fp16 values PV uses) in each of its rows.
+// On the matrix core this costs one MFMA per head and slice; as VALU row sums
+// (v_dot2_f32_f16) it took 12 instructions per slice that never overlap MFMA work.
 template <int HPW>
 __device__ __forceinline__ void pv_half8(const char* vs, int c, int col, int g,
-                                         const half8 (&pf)[HPW], floatx4 (&acc)[HPW][8]) {
+                                         const half8 (&pf)[HPW], floatx4 (&acc)[HPW][9]) {
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) {
     const u32x2 a0 = vt_read(vs, 32 * c, dt, col, g);
@@ -221,6 +224,9 @@ __device__ __forceinline__ void pv_half8(const char* vs, int c, int col, int g,
 #pragma unroll
     for (int j = 0; j < HPW; ++j) acc[j][dt] = mfma16x16x32(vf, pf[j], acc[j][dt]);
   }
+  const half8 ones = as_half8(u32x4{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u});
+#pragma unroll
+  for (int j = 0; j < HPW; ++j) acc[j][8] = mfma16x16x32(ones, pf[j], acc[j][8]);
 }
 
 // S^T = K Q^T for 32-key slice c of a resident K tile: s[j][t] holds keys
@@ -258,11 +264,11 @@ __device__ __forceinline__ void lane_max(const floatx4 (&s)[HPW][2], float (&lma
 // the softmax is unchanged.  The running state is the threshold t = m + lazy_raw, so the
 // test is one compare with no cross-lane step; when any lane's test fires (rare after
 // the first slices), every head's row max is reduced across the column's four lanes
-// and O and l are rescaled (alpha == 1 for heads whose threshold stays).
+// and O and l (accumulator tiles 0..8) are rescaled (alpha == 1 for heads whose
+// threshold stays).
 template <int HPW>
 __device__ __forceinline__ void maybe_move_max(const Params& p, const float (&lmax)[HPW],
-                                               float (&t_run)[HPW], float (&l_run)[HPW],
-                                               floatx4 (&acc)[HPW][8]) {
+                                               float (&t_run)[HPW], floatx4 (&acc)[HPW][9]) {
   bool move = false;
 #pragma unroll
   for (int j = 0; j < HPW; ++j) move |= lmax[j] > t_run[j];
@@ -274,9 +280,8 @@ __device__ __forceinline__ void maybe_move_max(const Params& p, const float (&lm
       const float t_new = rmax > t_old ? rmax + p.lazy_raw : t_old;
       const float alpha = fast_exp2((t_old - t_new) * p.scale_log2);
       t_run[j] = t_new;
-      l_run[j] *= alpha;
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) acc[j][dt] *= alpha;
+      for (int dt = 0; dt < 9; ++dt) acc[j][dt] *= alpha;
     }
   }
 }
@@ -297,31 +302,13 @@ __device__ __forceinline__ void softmax_exp(const Params& p, const floatx4 (&s)[
   }
 }
 
-// P as above, and l accumulates those fp16 values (v_dot2_f32_f16 against ones).
-template <int HPW>
-__device__ __forceinline__ void softmax_p(const Params& p, const floatx4 (&s)[HPW][2],
-                                          const float (&m_run)[HPW], float (&l_run)[HPW],
-                                          half8 (&pf)[HPW]) {
-  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-  softmax_exp<HPW>(p, s, m_run, pf);
-  const h2 one2 = {(half_t)1.f, (half_t)1.f};
-#pragma unroll
-  for (int j = 0; j < HPW; ++j) {
-    float psum = l_run[j];
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      psum = __builtin_amdgcn_fdot2(h2{pf[j][2 * e], pf[j][2 * e + 1]}, one2, psum, false);
-    l_run[j] = psum;
-  }
-}
-
 // A tile on the diagonal: masked (key > position, key >= seq_len), slices wholly above
 // this wave's last position skipped; one slice at a time.
 template <int HPW>
 __device__ __forceinline__ void consume_diag(const Params& p, const char* stage, int k0,
                                              int qpos, int wave_last, int col, int g,
                                              const half8 (&qf)[HPW][4], float (&m_run)[HPW],
-                                             float (&l_run)[HPW], floatx4 (&acc)[HPW][8]) {
+                                             floatx4 (&acc)[HPW][9]) {
   const char* ks = stage;
   const char* vs = stage + kTileBytes;
 #pragma unroll
@@ -340,9 +327,9 @@ __device__ __forceinline__ void consume_diag(const Params& p, const char* stage,
         }
     float lmax[HPW];
     lane_max<HPW>(s, lmax);
-    maybe_move_max<HPW>(p, lmax, m_run, l_run, acc);
+    maybe_move_max<HPW>(p, lmax, m_run, acc);
     half8 pf[HPW];
-    softmax_p<HPW>(p, s, m_run, l_run, pf);
+    softmax_exp<HPW>(p, s, m_run, pf);
     pv_half8<HPW>(vs, c, col, g, pf, acc);
   }
 }
@@ -354,8 +341,8 @@ __device__ __forceinline__ void consume_diag(const Params& p, const char* stage,
 template <int HPW>
 __device__ __forceinline__ void consume_full(const Params& p, const char* stage, int col,
                                              int g, const half8 (&qf)[HPW][4],
-                                             float (&m_run)[HPW], float (&l_run)[HPW],
-                                             floatx4 (&acc)[HPW][8], __amdgpu_buffer_rsrc_t kr,
+                                             float (&m_run)[HPW], floatx4 (&acc)[HPW][9],
+                                             __amdgpu_buffer_rsrc_t kr,
                                              __amdgpu_buffer_rsrc_t vr, char* nxt, int k0n,
                                              int w, int lane) {
   const char* ks = stage;
@@ -377,9 +364,9 @@ __device__ __forceinline__ void consume_full(const Params& p, const char* stage,
     for (int q = 0; q < kPerSlice; ++q) issue_tile_part(p, kr, vr, nxt, k0n, w, lane, kPerSlice * c + q);
     float lmax[HPW];
     lane_max<HPW>(s, lmax);
-    maybe_move_max<HPW>(p, lmax, m_run, l_run, acc);
+    maybe_move_max<HPW>(p, lmax, m_run, acc);
     half8 pf[HPW];
-    softmax_p<HPW>(p, s, m_run, l_run, pf);
+    softmax_exp<HPW>(p, s, m_run, pf);
     pv_half8<HPW>(vs, c, col, g, pf, acc);
   }
 }
@@ -427,14 +414,13 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(Params p) {
     }
   }
 
-  float m_run[HPW], l_run[HPW];
-  floatx4 acc[HPW][8];
+  float m_run[HPW];
+  floatx4 acc[HPW][9];  // per head: O^T head_dim rows 16dt..16dt+15 (dt < 8), l (dt = 8)
 #pragma unroll
   for (int j = 0; j < HPW; ++j) {
     m_run[j] = kNegBig;
-    l_run[j] = 0.f;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) acc[j][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int dt = 0; dt < 9; ++dt) acc[j][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
 
   // Key tiles: the diagonal tile (keys q0..q0+kKTile-1, this workgroup's own positions)
@@ -468,13 +454,13 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(Params p) {
   // at the start of tile 1, just before refilling stage 0, so the stores drain under tile
   // 1's work instead of under this tile's closing wait.
   if (pool && n == 1) write_pool(p, st0, pool_row, pool_entry, kvh, key0(0), tid);
-  consume_diag<HPW>(p, st0, key0(0), qpos, wave_last, col, g, qf, m_run, l_run, acc);
+  consume_diag<HPW>(p, st0, key0(0), qpos, wave_last, col, g, qf, m_run, acc);
   wait_vmcnt<0>();
   __builtin_amdgcn_s_barrier();
 #define FI_PREFILL_STEP(IDX, CUR, NXT)                                                    \
   {                                                                                       \
     if (pool && (IDX) == 1) write_pool_wave(p, NXT, pool_row, pool_entry, kvh, key0(0), w, lane); \
-    consume_full<HPW>(p, CUR, col, g, qf, m_run, l_run, acc, kr, vr, NXT, key0((IDX) + 1), \
+    consume_full<HPW>(p, CUR, col, g, qf, m_run, acc, kr, vr, NXT, key0((IDX) + 1),        \
                       w, lane);                                                           \
     wait_vmcnt<0>();                                                                      \
     __builtin_amdgcn_s_barrier();                                                         \
@@ -499,7 +485,7 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(Params p) {
   char* ostage = (w < 2 ? st0 : st1) + (w & 1) * (HPW * kRowsPerWave * kORow);
 #pragma unroll
   for (int j = 0; j < HPW; ++j) {
-    const float inv = 1.f / row4_sum(l_run[j]);
+    const float inv = 1.f / acc[j][8][0];  // every row of tile 8 holds the column's l
     char* orow = ostage + (j * kRowsPerWave + col) * kORow + 8 * g;
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) *(half4*)(orow + 32 * dt) = to_half4(acc[j][dt] * inv);
