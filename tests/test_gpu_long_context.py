@@ -1,4 +1,5 @@
-"""Paged decode at long contexts, up to the call's limit of 4096 × 1024 tokens (marked ``gpu``).
+"""Long contexts: paged decode up to the call's limit of 4096 × 1024 tokens, and a
+32,000-position prefill with the fused pool write (marked ``gpu``).
 
 Past 384 × 1024 tokens the partitions grow with the context (at most 1024 per row), up to
 4096 tokens each; the merge then combines hundreds of partials per (row, head).  One kv head
@@ -50,3 +51,35 @@ def test_paged_decode_long_context(hip, lens, bs):
     assert torch.isfinite(out).all()
     ref = OA.paged_attention(q.cpu(), kc.cpu(), vc.cpu(), table, bs, lens)
     assert float((out.float().cpu() - ref).abs().max()) <= ATOL
+
+
+def test_flash_prefill_long_sequence_with_pool(hip):
+    # batch 1 x 32,000 positions (500 query tiles, the last one partial), 24 / 8 heads:
+    # sampled rows of every head against the oracle, and the fused pool write gathered back
+    # through a shuffled table bit for bit
+    S, H, Hkv, bs = 32_000, 24, 8, 64
+    banner(f"flash prefill batch 1 x {S} with pool write")
+    from fast_infer_amd import flash_attention
+
+    g = torch.Generator(device=DEV).manual_seed(5)
+    q = torch.randn(1, S, H, D, device=DEV, generator=g).half().transpose(1, 2)
+    k = torch.randn(1, S, Hkv, D, device=DEV, generator=g).half()
+    v = torch.randn(1, S, Hkv, D, device=DEV, generator=g).half()
+    nb = math.ceil(S / bs)
+    N = nb + 3
+    table = torch.randperm(N, generator=torch.Generator().manual_seed(6)).int()[:nb].view(1, nb)
+    kc = torch.zeros(N, bs, Hkv, D, device=DEV, dtype=torch.float16)
+    vc = torch.zeros_like(kc)
+    out = flash_attention(q, k.transpose(1, 2), v.transpose(1, 2), k_cache=kc, v_cache=vc,
+                          block_table=table.to(DEV))
+    torch.cuda.synchronize()
+    rows = [0, 1, 63, 64, 4095, 20_001, S - 1]
+    ref = OA.causal_attention_rows(q.cpu(), k.transpose(1, 2).cpu(), v.transpose(1, 2).cpu(), rows)
+    got = out[:, :, rows].float().cpu()
+    assert float((got - ref).abs().max()) <= ATOL
+    t = torch.arange(S)
+    slot = (table[0, t // bs].long() * bs + t % bs).to(DEV)
+    assert torch.equal(kc.view(-1, Hkv, D)[slot], k[0])
+    assert torch.equal(vc.view(-1, Hkv, D)[slot], v[0])
+    unused = sorted(set(range(N)) - set(table[0].tolist()))
+    assert float(kc[unused].abs().max()) == 0.0 and float(vc[unused].abs().max()) == 0.0
