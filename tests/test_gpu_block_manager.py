@@ -101,11 +101,14 @@ def test_errors_recorded_and_check_raises(hip):
     cache.check()  # clear again
 
 
-def test_continuous_batching_decode_end_to_end(hip):
-    banner("continuous batching: rope + pool write + paged decode")
+@pytest.mark.parametrize("bs", [16, 8, 5])
+def test_continuous_batching_decode_end_to_end(hip, bs):
+    # block sizes 8 and 5 run the decode kernel's per-row block addressing
+    banner(f"continuous batching: rope + pool write + paged decode, block_size {bs}")
     from fast_infer_amd import PagedKVCache, paged_attention, rope_store_kv
 
-    L, Hq, Hkv, D, bs, B, N, maxlen = 2, 8, 2, 128, 16, 6, 90, 256
+    L, Hq, Hkv, D, B, maxlen = 2, 8, 2, 128, 6, 256
+    N = 90 * 16 // bs
     cache = PagedKVCache(L, Hkv, D, maxlen, bs, DEV, max_batch=B, num_blocks=N)
     m = OB.OracleBlockManager(N, cache.max_blocks_per_seq, B, bs)
     cos, sin = OR.precompute_freqs(D, maxlen)
