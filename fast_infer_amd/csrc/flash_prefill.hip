@@ -17,8 +17,8 @@
 //   * 64-key K/V tiles are copied global->LDS by the buffer unit (no register staging),
 //     double-buffered; each slice issues its share of the next tile's copy;
 //   * the diagonal tile is processed first; when a pool is given, the workgroup that
-//     owns a 64-token block of K/V also copies it into the paged pool (the write of
-//     model.py:176-183), so the scatter costs no extra read.
+//     owns a 64-token tile of K/V also copies it into the paged pool (the write of
+//     model.py:176-183, any block size), so the scatter costs no extra read.
 #include "common.h"
 
 namespace fi {
@@ -63,9 +63,10 @@ struct Params {
   int v_records;
   int k_row_bytes;   // k_ss * 2 (spans are checked to fit 31 bits)
   int v_row_bytes;
-  half_t* k_cache;   // optional pool (block_size 64)
+  half_t* k_cache;   // optional pool [num_pool_blocks, block_size, num_kv_heads, head_dim]
   half_t* v_cache;
   int64_t num_pool_blocks;
+  int block_size;
   const int32_t* block_table;
   int64_t bt_stride;
   int max_blocks_per_seq;
@@ -151,10 +152,37 @@ __device__ __forceinline__ int64_t pool_block_base(const Params& p, bool row_ok,
   return (int64_t)entry * kPoolBlock * p.num_kv_heads * p.head_dim + (int64_t)kvh * p.head_dim;
 }
 
-// Copy the resident diagonal tile from LDS into its pool block.
-template <int NT = kThreads>
+// Any other block size: lane r of every wave holds the table entry of row r of the diagonal
+// tile (-1 when the row is past seq_len or the table), loaded by the caller.  The element
+// offset of row `slot`'s chunk `ch` in the pool, or -1 when the row has no valid block.
+// Every lane of the wave must call this (the entry comes from lane `slot` by ds_bpermute).
+__device__ __forceinline__ int64_t pool_row_dst(const Params& p, int entry, int kvh, int k0,
+                                                int slot, int ch) {
+  const int e = __builtin_amdgcn_ds_bpermute(slot << 2, entry);
+  if (e < 0 || e >= p.num_pool_blocks) return -1;
+  const int tok = k0 + slot;
+  const int64_t row = (int64_t)e * p.block_size + tok % p.block_size;
+  return (row * p.num_kv_heads + kvh) * p.head_dim + 8 * ch;
+}
+
+// Copy the resident diagonal tile from LDS into the pool (kRows: any block size other
+// than 64, one entry per row).
+template <bool kRows, int NT = kThreads>
 __device__ __forceinline__ void write_pool(const Params& p, const char* stage, bool row_ok,
                                            int entry, int kvh, int k0, int tid) {
+  if (kRows) {
+    asm volatile("" : "+v"(entry));  // the wait for the entries' loads stays here
+#pragma unroll
+    for (int j = 0; j < kKTile * 16 / NT; ++j) {
+      const int f = NT * j + tid;
+      const int slot = f >> 4, ch = f & 15;
+      const int64_t dst = pool_row_dst(p, entry, kvh, k0, slot, ch);
+      if (k0 + slot >= p.seq_len || ch >= p.d_chunks || dst < 0) continue;
+      *(u32x4*)(p.k_cache + dst) = *(const u32x4*)(stage + k_off(slot, ch));
+      *(u32x4*)(p.v_cache + dst) = *(const u32x4*)(stage + kTileBytes + v_off(slot, ch));
+    }
+    return;
+  }
   const int64_t base = pool_block_base(p, row_ok, entry, kvh);
   if (base < 0) return;
   const int64_t row_stride = (int64_t)p.num_kv_heads * p.head_dim;
@@ -371,7 +399,10 @@ __device__ __forceinline__ void consume_full(const Params& p, const char* stage,
   }
 }
 
-template <int HPW>  // query heads per workgroup
+// HPW: query heads per workgroup.  kRows: a fused pool write with a block size other than 64 (the diagonal tile then spans
+// several pool blocks or part of one; it is written at the start, before the accumulators
+// are live, as that write needs registers for per-row addresses).
+template <int HPW, bool kRows>
 __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(Params p) {
   // two pipeline stages of one K tile + one V tile each (distinct objects, so the
   // compiler tracks their DMA writes separately)
@@ -431,10 +462,12 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(Params p) {
     return (idx == 0 ? qt : idx - 1) * kKTile;
   };
   const bool pool = p.k_cache != nullptr && hsub == 0;
-  // The pool block of the diagonal tile: logical block qt of row b.  Its table entry is
-  // loaded right after the first copies go out and first used in the pool write, so the
-  // load's latency hides under the first tile's.
+  // The pool block of the diagonal tile: logical block qt of row b (block_size 64).  Its
+  // table entry is loaded right after the first copies go out and first used in the pool
+  // write, so the load's latency hides under the first tile's.  With another block size
+  // lane r loads the entry of the block holding position q0 + r instead.
   const bool pool_row = pool && qt < p.max_blocks_per_seq;
+  const bool pool_rows = pool && kRows;
   int pool_entry = -1;
   const int wave_last = q0 + kRowsPerWave * w + kRowsPerWave - 1;  // last position of the wave
 
@@ -447,19 +480,27 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(Params p) {
   // and the first wait covers tile 0 only (loads complete in issue order).
   issue_tile(p, kr, vr, st0, key0(0), w, lane);
   issue_tile(p, kr, vr, st1, key0(1), w, lane);
-  if (pool_row) pool_entry = p.block_table[(int64_t)b * p.bt_stride + qt];
+  if (pool_rows) {
+    const int tok = q0 + lane;
+    const int lb = tok / p.block_size;
+    if (tok < p.seq_len && lb < p.max_blocks_per_seq)
+      pool_entry = p.block_table[(int64_t)b * p.bt_stride + lb];
+  } else if (pool_row) {
+    pool_entry = p.block_table[(int64_t)b * p.bt_stride + qt];
+  }
   wait_vmcnt<kIssuePerTile>();
   __builtin_amdgcn_s_barrier();
   // The pool copy of the diagonal tile: with a following tile, each wave stores its share
   // at the start of tile 1, just before refilling stage 0, so the stores drain under tile
   // 1's work instead of under this tile's closing wait.
-  if (pool && n == 1) write_pool(p, st0, pool_row, pool_entry, kvh, key0(0), tid);
+  if (pool && (n == 1 || kRows)) write_pool<kRows>(p, st0, pool_row, pool_entry, kvh, key0(0), tid);
   consume_diag<HPW>(p, st0, key0(0), qpos, wave_last, col, g, qf, m_run, acc);
   wait_vmcnt<0>();
   __builtin_amdgcn_s_barrier();
 #define FI_PREFILL_STEP(IDX, CUR, NXT)                                                    \
   {                                                                                       \
-    if (pool && (IDX) == 1) write_pool_wave(p, NXT, pool_row, pool_entry, kvh, key0(0), w, lane); \
+    if (!kRows && pool && (IDX) == 1)                                                     \
+      write_pool_wave(p, NXT, pool_row, pool_entry, kvh, key0(0), w, lane);              \
     consume_full<HPW>(p, CUR, col, g, qf, m_run, acc, kr, vr, NXT, key0((IDX) + 1),        \
                       w, lane);                                                           \
     wait_vmcnt<0>();                                                                      \
@@ -561,10 +602,9 @@ extern "C" int fi_flash_attention_fwd(const void* q, const void* k, const void* 
       set_error("fi_flash_attention_fwd: pool write needs v_cache and block_table");
       return FI_ERR_INVALID;
     }
-    if (block_size != kPoolBlock) {
-      set_error("fi_flash_attention_fwd: fused pool write needs block_size %d (got %lld)",
-                kPoolBlock, (long long)block_size);
-      return FI_ERR_UNSUPPORTED;
+    if (block_size <= 0 || block_size > (1 << 20)) {
+      set_error("fi_flash_attention_fwd: invalid pool block_size %lld", (long long)block_size);
+      return FI_ERR_INVALID;
     }
     if (((uintptr_t)k_cache | (uintptr_t)v_cache) & 15u) {
       set_error("fi_flash_attention_fwd: pools must be 16-byte aligned");
@@ -612,6 +652,7 @@ extern "C" int fi_flash_attention_fwd(const void* q, const void* k, const void* 
   p.k_cache = (half_t*)k_cache;
   p.v_cache = (half_t*)v_cache;
   p.num_pool_blocks = num_pool_blocks;
+  p.block_size = (int)block_size;
   p.block_table = block_table;
   p.bt_stride = bt_stride;
   p.max_blocks_per_seq = (int)max_blocks_per_seq;
@@ -635,16 +676,15 @@ extern "C" int fi_flash_attention_fwd(const void* q, const void* k, const void* 
   }
   const dim3 grid((unsigned)gx, (unsigned)p.num_q_tiles);
   const dim3 block(kThreads);
-  switch (hpw) {
-    case 3:
-      hipLaunchKernelGGL(fwd_kernel<3>, grid, block, 0, (hipStream_t)stream, p);
-      break;
-    case 2:
-      hipLaunchKernelGGL(fwd_kernel<2>, grid, block, 0, (hipStream_t)stream, p);
-      break;
-    default:
-      hipLaunchKernelGGL(fwd_kernel<1>, grid, block, 0, (hipStream_t)stream, p);
-      break;
+  const bool rows = k_cache && block_size != kPoolBlock;
+  const hipStream_t st = (hipStream_t)stream;
+  switch (hpw * 2 + (rows ? 1 : 0)) {
+    case 6: hipLaunchKernelGGL((fwd_kernel<3, false>), grid, block, 0, st, p); break;
+    case 7: hipLaunchKernelGGL((fwd_kernel<3, true>), grid, block, 0, st, p); break;
+    case 4: hipLaunchKernelGGL((fwd_kernel<2, false>), grid, block, 0, st, p); break;
+    case 5: hipLaunchKernelGGL((fwd_kernel<2, true>), grid, block, 0, st, p); break;
+    case 3: hipLaunchKernelGGL((fwd_kernel<1, true>), grid, block, 0, st, p); break;
+    default: hipLaunchKernelGGL((fwd_kernel<1, false>), grid, block, 0, st, p); break;
   }
   return check_launch("fi_flash_attention_fwd");
 }

@@ -90,9 +90,9 @@ FI_API const char* fi_last_error(void);
  *
  * Optional fused pool write (k_cache != NULL): additionally copies k[b, :, t, :] and
  * v[b, :, t, :] into k_cache/v_cache at block block_table[b, t / block_size], slot
- * t % block_size, for every t < seq_len — the write of model.py:176-183.  The fused
- * path needs block_size == 64; other block sizes return FI_ERR_UNSUPPORTED (use
- * fi_kv_store).  Table entries outside [0, num_pool_blocks) are skipped.
+ * t % block_size, for every t < seq_len — the write of model.py:176-183.  Any block_size
+ * from 1 to 2^20 (64, the reference's, is the fastest path).  Table entries outside
+ * [0, num_pool_blocks), and tokens past the table's max_blocks_per_seq blocks, are skipped.
  */
 FI_API int fi_flash_attention_fwd(const void* q, const void* k, const void* v, void* o,
                            int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,

@@ -90,10 +90,10 @@ def test_invalid_arguments(lib):
     rc = lib.fi_flash_attention_fwd(18, 16, 16, 16, 1, 8, 8, 8, 128, *([8] * 12), 1.0,
                                     None, None, 0, 64, None, 0, 0, None)
     assert rc == _lib.FI_ERR_INVALID and b"aligned" in lib.fi_last_error()
-    # fused pool write with another block size
+    # fused pool write with block size 0
     rc = lib.fi_flash_attention_fwd(16, 16, 16, 16, 1, 8, 8, 8, 128, *([8] * 12), 1.0,
-                                    32, 32, 4, 32, 64, 4, 4, None)
-    assert rc == _lib.FI_ERR_UNSUPPORTED
+                                    32, 32, 4, 0, 64, 4, 4, None)
+    assert rc == _lib.FI_ERR_INVALID and b"block_size" in lib.fi_last_error()
     # decode block size 0
     rc = lib.fi_paged_attention_fwd(16, 8, 8, 16, 16, 1, 0, 1, 16, 1, 1, None, 1, 32, 8, 8,
                                     1, 1, 128, 1.0, None, 0, None)

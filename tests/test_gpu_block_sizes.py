@@ -11,7 +11,8 @@ that are -1 or outside the pool dropping out of the softmax, and, at the full de
 (batch 32, contexts 512..4096), bit-identical outputs for one logical context stored with
 block sizes 64, 48, 8 and 1 (the partitions and tiles are laid over token positions, so
 the block size may only change where a row's bytes come from), and bit-identical outputs of
-the per-row path on 4.3 GB pools and the per-lane path on a small one.
+the per-row path on 4.3 GB pools and the per-lane path on a small one.  The fused prefill
+pool write at block sizes other than 64 is checked bit for bit against the oracle scatter.
 """
 
 import math
@@ -202,3 +203,40 @@ def test_paged_decode_block_size_graph_replay(hip, bs):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, ref), rep
+
+
+@pytest.mark.parametrize("bs", [1, 8, 24, 100, 128])
+@pytest.mark.parametrize("S,D", [(1, 128), (300, 128), (700, 64)])
+def test_flash_prefill_pool_write_block_size(hip, bs, S, D):
+    # the fused prefill pool write at block sizes other than 64: the written slots equal the
+    # scatter of K/V bit for bit, every other slot keeps its bytes, the output is the plain
+    # call's (a row's table is one block short, so its last tokens are not written)
+    banner(f"flash prefill fused pool write, block_size {bs}, S={S}, head_dim {D}")
+    import numpy as np
+
+    from fast_infer_amd import flash_attention
+    from oracle import kv as OK
+
+    B, H, Hkv = 2, 6, 2
+    g = torch.Generator().manual_seed(bs * 7 + S)
+    q = torch.randn(B, S, H, D, generator=g).half().to(DEV).transpose(1, 2)
+    k = torch.randn(B, S, Hkv, D, generator=g).half().to(DEV)
+    v = torch.randn(B, S, Hkv, D, generator=g).half().to(DEV)
+    nb = math.ceil(S / bs)
+    N = 2 * nb + 3
+    perm = torch.randperm(N, generator=torch.Generator().manual_seed(bs)).int()
+    table = perm[:2 * nb].view(2, nb).clone()
+    if nb > 1:
+        table[1, nb - 1] = -1  # row 1's last block missing
+    kc0 = torch.randn(N, bs, Hkv, D, generator=g).half()
+    vc0 = torch.randn(N, bs, Hkv, D, generator=g).half()
+    kc, vc = kc0.to(DEV), vc0.to(DEV)
+    out = flash_attention(q, k.transpose(1, 2), v.transpose(1, 2), k_cache=kc, v_cache=vc,
+                          block_table=table.to(DEV), block_size=bs)
+    plain = flash_attention(q, k.transpose(1, 2), v.transpose(1, 2))
+    torch.cuda.synchronize()
+    assert torch.equal(out, plain)
+    ek, ev = kc0.numpy().copy(), vc0.numpy().copy()
+    OK.scatter(ek, ev, table.tolist(), k.cpu().numpy(), v.cpu().numpy(), 0, bs)
+    assert np.array_equal(kc.cpu().numpy().view(np.uint16), ek.view(np.uint16))
+    assert np.array_equal(vc.cpu().numpy().view(np.uint16), ev.view(np.uint16))
