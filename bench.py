@@ -557,7 +557,7 @@ def main():
             "roofline": {"bound": "mfma", "achieved": round(pre["tflops"], 2),
                          "peak": R.FP16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(pre["tflops"] / R.FP16_MFMA_PEAK_TFLOPS, 4),
-                         "traffic": _traffic("prefill_b4_s4096"), "kernel": "fwd_kernel<3>",
+                         "traffic": _traffic("prefill_b4_s4096"), "kernel": "fwd_kernel<3, false>",
                          "algorithmic_flops": pre["flops"],
                          "pool_write_bytes": pre["scatter_bytes"]},
         }
