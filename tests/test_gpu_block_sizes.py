@@ -240,3 +240,37 @@ def test_flash_prefill_pool_write_block_size(hip, bs, S, D):
     OK.scatter(ek, ev, table.tolist(), k.cpu().numpy(), v.cpu().numpy(), 0, bs)
     assert np.array_equal(kc.cpu().numpy().view(np.uint16), ek.view(np.uint16))
     assert np.array_equal(vc.cpu().numpy().view(np.uint16), ev.view(np.uint16))
+
+
+@pytest.mark.parametrize("bs", [8, 64])
+def test_flash_prefill_pool_write_narrow_table(hip, bs):
+    # a table one block narrower than the sequence needs, and an entry outside the pool:
+    # tokens past the table or in that block are not written, everything else is
+    banner(f"flash prefill fused pool write, block_size {bs}, narrow table")
+    import numpy as np
+
+    from fast_infer_amd import flash_attention
+    from oracle import kv as OK
+
+    B, S, H, Hkv, D = 2, 200, 6, 2, 128
+    g = torch.Generator().manual_seed(bs + 99)
+    q = torch.randn(B, S, H, D, generator=g).half().to(DEV).transpose(1, 2)
+    k = torch.randn(B, S, Hkv, D, generator=g).half().to(DEV)
+    v = torch.randn(B, S, Hkv, D, generator=g).half().to(DEV)
+    nb = math.ceil(S / bs)
+    N = 2 * nb + 1
+    perm = torch.randperm(N, generator=torch.Generator().manual_seed(bs)).int()
+    table = perm[:2 * nb].view(2, nb)[:, :nb - 1].clone()  # one block short
+    table[0, 1] = 10 ** 6                                  # outside the pool
+    kc0 = torch.randn(N, bs, Hkv, D, generator=g).half()
+    vc0 = torch.randn(N, bs, Hkv, D, generator=g).half()
+    kc, vc = kc0.to(DEV), vc0.to(DEV)
+    out = flash_attention(q, k.transpose(1, 2), v.transpose(1, 2), k_cache=kc, v_cache=vc,
+                          block_table=table.to(DEV), block_size=bs)
+    plain = flash_attention(q, k.transpose(1, 2), v.transpose(1, 2))
+    torch.cuda.synchronize()
+    assert torch.equal(out, plain)
+    ek, ev = kc0.numpy().copy(), vc0.numpy().copy()
+    OK.scatter(ek, ev, table.tolist(), k.cpu().numpy(), v.cpu().numpy(), 0, bs)
+    assert np.array_equal(kc.cpu().numpy().view(np.uint16), ek.view(np.uint16))
+    assert np.array_equal(vc.cpu().numpy().view(np.uint16), ev.view(np.uint16))
