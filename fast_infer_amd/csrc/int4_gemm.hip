@@ -744,25 +744,27 @@ __global__ __launch_bounds__(256) void reduce_kernel(const float* partial, int s
 // arithmetic: amax = max|w| over the group (fp16), clamped below at fp16(1e-6); scale =
 // fp16(fp32(amax) * fp32(1/7)) (torch multiplies by the reciprocal when a CUDA tensor is
 // divided by a Python scalar); q = round_half_even(fp16(fp32(w) / fp32(scale))), clamped to
-// [-8, 7].  16 lanes per group, 8 values per lane.
+// [-8, 7].  gs / 8 lanes per group (gs a power of two from 8 to 512), 8 values per lane;
+// a group's lanes are consecutive lanes of one wave, so they enter and leave the loop together.
 __global__ __launch_bounds__(256) void quantize_kernel(const half_t* w, int64_t w_stride, int N,
-                                                       int K, uint8_t* packed,
+                                                       int K, int gs, uint8_t* packed,
                                                        int64_t p_stride, half_t* scales,
                                                        int64_t s_stride) {
-  const int groups = K / kGroup;
+  const int groups = K / gs;
+  const int lanes = gs / 8;          // per group
+  const int shift = __builtin_ctz(lanes);
   const int64_t total = (int64_t)N * groups;
-  const int lane16 = threadIdx.x & 15;
-  for (int64_t gi = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4; gi < total;
-       gi += ((int64_t)gridDim.x * blockDim.x) >> 4) {
+  const int lane16 = threadIdx.x & (lanes - 1);
+  for (int64_t gi = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> shift; gi < total;
+       gi += ((int64_t)gridDim.x * blockDim.x) >> shift) {
     const int nrow = (int)(gi / groups);
     const int g = (int)(gi - (int64_t)nrow * groups);
     const half8 v = as_half8(
-        *(const u32x4*)(w + (int64_t)nrow * w_stride + g * kGroup + lane16 * 8));
+        *(const u32x4*)(w + (int64_t)nrow * w_stride + (int64_t)g * gs + lane16 * 8));
     float amax = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf((float)v[e]));
-#pragma unroll
-    for (int d = 1; d < 16; d <<= 1) amax = fmaxf(amax, __shfl_xor(amax, d, 16));
+    for (int d = 1; d < lanes; d <<= 1) amax = fmaxf(amax, __shfl_xor(amax, d, lanes));
     const float lo = (float)(half_t)1e-6f;
     amax = fmaxf(amax, lo);
     const half_t scale = (half_t)(amax * (1.0f / 7.0f));
@@ -774,15 +776,16 @@ __global__ __launch_bounds__(256) void quantize_kernel(const half_t* w, int64_t 
       const float qr = fminf(fmaxf(__builtin_rintf(qf), -8.f), 7.f);
       word |= ((uint32_t)(int)qr & 0xFu) << (4 * e);
     }
-    *(uint32_t*)(packed + (int64_t)nrow * p_stride + g * (kGroup / 2) + lane16 * 4) = word;
+    *(uint32_t*)(packed + (int64_t)nrow * p_stride + (int64_t)g * (gs / 2) + lane16 * 4) = word;
     if (lane16 == 0) scales[(int64_t)nrow * s_stride + g] = scale;
   }
 }
 
-// matmul.py:309-326 (_dequant_storage): W = fp16(q * scale), 8 values per thread.
+// matmul.py:309-326 (_dequant_storage): W = fp16(q * scale), 8 values per thread (gs, the
+// group size, a multiple of 8).
 __global__ __launch_bounds__(256) void dequantize_kernel(const uint8_t* packed, int64_t p_stride,
                                                          const half_t* scales, int64_t s_stride,
-                                                         int N, int K, half_t* w,
+                                                         int N, int K, int gs, half_t* w,
                                                          int64_t w_stride) {
   const int per_row = K / 8;
   const int64_t total = (int64_t)N * per_row;
@@ -791,7 +794,7 @@ __global__ __launch_bounds__(256) void dequantize_kernel(const uint8_t* packed, 
     const int nrow = (int)(i / per_row);
     const int c = (int)(i - (int64_t)nrow * per_row);
     const uint32_t d = *(const uint32_t*)(packed + (int64_t)nrow * p_stride + c * 4);
-    const half_t s = scales[(int64_t)nrow * s_stride + (c * 8) / kGroup];
+    const half_t s = scales[(int64_t)nrow * s_stride + (c * 8) / gs];
     *(u32x4*)(w + (int64_t)nrow * w_stride + c * 8) = as_u32x4(dequant8(d, half2_t{s, s}));
   }
 }
@@ -1086,7 +1089,7 @@ int run_linear(const char* fn, const void* x, int64_t x_stride, int64_t M, int64
       const int64_t blocks = std::min<int64_t>((items + 255) / 256, 65536);
       hipLaunchKernelGGL(dequantize_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
                          (const uint8_t*)w, w_stride, (const half_t*)scales, s_stride, (int)N,
-                         (int)K, deq, K);
+                         (int)K, kGroup, deq, K);
       w16 = deq;
       ldw = K;
     }
@@ -1181,12 +1184,12 @@ extern "C" int fi_int4_quantize(const void* w, int64_t w_stride, int64_t N, int6
   using namespace fi;
   using namespace fi::gemm;
   clear_error();
-  if (groupsize != kGroup) {
-    set_error("fi_int4_quantize: groupsize %lld not supported (only %d)", (long long)groupsize,
-              kGroup);
+  if (groupsize < 8 || groupsize > 512 || (groupsize & (groupsize - 1))) {
+    set_error("fi_int4_quantize: groupsize %lld not supported (a power of two from 8 to 512)",
+              (long long)groupsize);
     return FI_ERR_UNSUPPORTED;
   }
-  if (N < 0 || K < 0 || K % kGroup || N >= (1ll << 30) || K >= (1ll << 30)) {
+  if (N < 0 || K < 0 || K % groupsize || N >= (1ll << 30) || K >= (1ll << 30)) {
     set_error("fi_int4_quantize: invalid sizes N %lld K %lld", (long long)N, (long long)K);
     return FI_ERR_INVALID;
   }
@@ -1196,14 +1199,15 @@ extern "C" int fi_int4_quantize(const void* w, int64_t w_stride, int64_t N, int6
     return FI_ERR_INVALID;
   }
   if (((uintptr_t)w & 15) || w_stride % 8 || w_stride < K || ((uintptr_t)packed & 3) ||
-      p_stride % 4 || p_stride < K / 2 || ((uintptr_t)scales & 1) || s_stride < K / kGroup) {
+      p_stride % 4 || p_stride < K / 2 || ((uintptr_t)scales & 1) || s_stride < K / groupsize) {
     set_error("fi_int4_quantize: misaligned rows or short strides");
     return FI_ERR_INVALID;
   }
-  const int64_t lanes = N * (K / kGroup) * 16;
+  const int64_t lanes = N * K / 8;  // gs / 8 per group
   const int64_t blocks = std::min<int64_t>((lanes + 255) / 256, 65536);
   hipLaunchKernelGGL(quantize_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
-                     (const half_t*)w, w_stride, (int)N, (int)K, (uint8_t*)packed, p_stride,
+                     (const half_t*)w, w_stride, (int)N, (int)K, (int)groupsize,
+                     (uint8_t*)packed, p_stride,
                      (half_t*)scales, s_stride);
   return check_launch("fi_int4_quantize");
 }
@@ -1214,12 +1218,12 @@ extern "C" int fi_int4_dequantize(const void* packed, int64_t p_stride, const vo
   using namespace fi;
   using namespace fi::gemm;
   clear_error();
-  if (groupsize != kGroup) {
-    set_error("fi_int4_dequantize: groupsize %lld not supported (only %d)",
-              (long long)groupsize, kGroup);
+  if (groupsize < 8 || groupsize > 512 || (groupsize & (groupsize - 1))) {
+    set_error("fi_int4_dequantize: groupsize %lld not supported (a power of two from 8 to 512)",
+              (long long)groupsize);
     return FI_ERR_UNSUPPORTED;
   }
-  if (N < 0 || K < 0 || K % kGroup || N >= (1ll << 30) || K >= (1ll << 30)) {
+  if (N < 0 || K < 0 || K % groupsize || N >= (1ll << 30) || K >= (1ll << 30)) {
     set_error("fi_int4_dequantize: invalid sizes N %lld K %lld", (long long)N, (long long)K);
     return FI_ERR_INVALID;
   }
@@ -1229,7 +1233,7 @@ extern "C" int fi_int4_dequantize(const void* packed, int64_t p_stride, const vo
     return FI_ERR_INVALID;
   }
   if (((uintptr_t)w & 15) || w_stride % 8 || w_stride < K || ((uintptr_t)packed & 3) ||
-      p_stride % 4 || p_stride < K / 2 || ((uintptr_t)scales & 1) || s_stride < K / kGroup) {
+      p_stride % 4 || p_stride < K / 2 || ((uintptr_t)scales & 1) || s_stride < K / groupsize) {
     set_error("fi_int4_dequantize: misaligned rows or short strides");
     return FI_ERR_INVALID;
   }
@@ -1237,6 +1241,7 @@ extern "C" int fi_int4_dequantize(const void* packed, int64_t p_stride, const vo
   const int64_t blocks = std::min<int64_t>((items + 255) / 256, 65536);
   hipLaunchKernelGGL(dequantize_kernel, dim3((unsigned)blocks), dim3(256), 0,
                      (hipStream_t)stream, (const uint8_t*)packed, p_stride,
-                     (const half_t*)scales, s_stride, (int)N, (int)K, (half_t*)w, w_stride);
+                     (const half_t*)scales, s_stride, (int)N, (int)K, (int)groupsize,
+                     (half_t*)w, w_stride);
   return check_launch("fi_int4_dequantize");
 }

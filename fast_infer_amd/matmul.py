@@ -15,6 +15,8 @@ import torch
 
 from . import _lib
 
+PACKED_GROUP = 128  # the group size the packed-weight kernels read (the reference's)
+
 
 def _need_cuda(name: str, t: torch.Tensor) -> None:
     if t.device.type != "cuda":
@@ -58,8 +60,11 @@ def int4_matmul(x: torch.Tensor, w, scales=None, groupsize: int = 128, *,
     K/groupsize])`` or an fp16 ``[N, K]`` tensor; ``scales`` is ignored as in the
     reference.  Accumulation is fp32, the output rounded to fp16 once.  ``workspace``
     (optional) must not be shared by calls that overlap in time; by default one cached
-    workspace per device and stream is used."""
+    workspace per device and stream is used.  The packed kernels read 128-wide groups (the
+    reference's); packed weights with another group size are dequantized first (the same
+    fp16 values) and take the fp16 form."""
     _need_cuda("x", x)
+    w = _other_group_size(w, groupsize)
     N, K, wt, w_stride, s_ptr, s_stride, _keep = _weight_args(w, groupsize)
     if x.shape[-1] != K:
         raise ValueError(f"x has K = {x.shape[-1]}, the weight K = {K}")
@@ -85,6 +90,13 @@ def int4_matmul(x: torch.Tensor, w, scales=None, groupsize: int = 128, *,
                             ws_bytes, stream)
     _lib.check(rc, "int4_matmul")
     return out.reshape(*lead, N)
+
+
+def _other_group_size(w, groupsize: int):
+    """Packed weights whose group size is not 128 as the dequantized fp16 tensor."""
+    if isinstance(w, tuple) and groupsize != PACKED_GROUP:
+        return dequantize_int4(w[0], w[1], groupsize)
+    return w
 
 
 def _weight_args(w, groupsize: int):
@@ -136,8 +148,10 @@ def rms_norm_int4_matmul(x: torch.Tensor, norm_weight: torch.Tensor, w, eps: flo
                          groupsize: int = 128, *,
                          workspace: torch.Tensor | None = None) -> torch.Tensor:
     """``int4_matmul(rms_norm(x, norm_weight, eps), w)`` in one call (model.py:82 and the
-    QKV projection after it): for few rows the norm is applied inside the GEMM."""
+    QKV projection after it): for few rows the norm is applied inside the GEMM.  Packed
+    weights with a group size other than 128 take the fp16 form, as in ``int4_matmul``."""
     _need_cuda("x", x)
+    w = _other_group_size(w, groupsize)
     N, K, wt, w_stride, s_ptr, s_stride, _keep = _weight_args(w, groupsize)
     if x.shape[-1] != K or norm_weight.shape != (K,):
         raise ValueError(f"x {tuple(x.shape)} / norm weight {tuple(norm_weight.shape)} do not "
@@ -170,7 +184,8 @@ def rms_norm_int4_matmul(x: torch.Tensor, norm_weight: torch.Tensor, w, eps: flo
 def quantize_int4_groupwise(w: torch.Tensor, groupsize: int = 128
                             ) -> tuple[torch.Tensor, torch.Tensor]:
     """loader.py:9-41: fp16 ``w [N, K]`` -> (packed int8 ``[N, K/2]``, scales fp16
-    ``[N, K/groupsize]``), bit-exact with the reference's arithmetic on a CUDA device."""
+    ``[N, K/groupsize]``), bit-exact with the reference's arithmetic on a CUDA device;
+    ``groupsize`` a power of two from 8 to 512."""
     _need_cuda("w", w)
     if w.dtype != torch.float16 or w.dim() != 2:
         raise TypeError("w must be a 2-D float16 tensor")

@@ -300,8 +300,9 @@ FI_API int fi_kv_reset(int32_t* block_table, int64_t bt_stride, int64_t max_bloc
  *            w_stride elements.
  *   out    : fp16 [M, N], row stride out_stride elements.
  *   Each weight is fp16(q * scale) exactly as the reference dequantizes it; products are
- *   accumulated in fp32 and rounded to fp16 once.  groupsize must be 128 and K a multiple
- *   of 128.  Some shapes split K: then a workspace of
+ *   accumulated in fp32 and rounded to fp16 once.  Packed weights need groupsize 128 (the
+ *   reference's) and K a multiple of 128; for another group size, dequantize with
+ *   fi_int4_dequantize and pass the fp16 weight.  Some shapes split K: then a workspace of
  *   fi_int4_matmul_workspace_size(M, N, K) bytes (enough for either weight form) is
  *   required (FI_ERR_WORKSPACE otherwise); calls that overlap in time must not share one.
  */
@@ -338,18 +339,20 @@ FI_API int fi_rmsnorm_int4_matmul(const void* x, int64_t x_stride, int64_t M, in
 
 /*
  * quantize_int4_groupwise (loader.py:9-41) on the device, bit-exact with the reference's
- * fp16 tensor arithmetic on a CUDA device: amax = max |w| over each 128-wide group,
- * clamped below at fp16(1e-6); scale = fp16(fp32(amax) * fp32(1/7)); q =
+ * fp16 tensor arithmetic on a CUDA device: amax = max |w| over each group of groupsize
+ * consecutive k, clamped below at fp16(1e-6); scale = fp16(fp32(amax) * fp32(1/7)); q =
  * round_half_even(fp16(fp32(w) / fp32(scale))) clamped to [-8, 7], packed two per byte.
+ * groupsize: a power of two from 8 to 512 (128 in the reference), dividing K.
  *   w fp16 [N, K] (row stride w_stride elements, 16-byte aligned rows);
- *   packed int8 [N, K/2] (row stride p_stride bytes), scales fp16 [N, K/128].
+ *   packed int8 [N, K/2] (row stride p_stride bytes), scales fp16 [N, K/groupsize].
  */
 FI_API int fi_int4_quantize(const void* w, int64_t w_stride, int64_t N, int64_t K,
                      int64_t groupsize, void* packed, int64_t p_stride, void* scales,
                      int64_t s_stride, void* stream);
 
 /*
- * _dequant_storage (kernels/matmul.py:309-326): w[n, k] = fp16(q[n, k] * scale[n, k/128]).
+ * _dequant_storage (kernels/matmul.py:309-326): w[n, k] = fp16(q[n, k] *
+ * scale[n, k / groupsize]); groupsize as for fi_int4_quantize.
  */
 FI_API int fi_int4_dequantize(const void* packed, int64_t p_stride, const void* scales,
                        int64_t s_stride, int64_t N, int64_t K, int64_t groupsize, void* w,

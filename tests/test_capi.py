@@ -187,8 +187,15 @@ def test_int4_validation(lib):
     assert need > 0
     assert lib.fi_int4_matmul(16, 3072, 40, 3072, 16, 1536, 16, 24, 5120, 128, 16, 5120, None,
                               0, None) == _lib.FI_ERR_WORKSPACE
-    assert lib.fi_int4_quantize(16, 256, 4, 256, 64, 16, 128, 16, 2, None) == \
+    # quantize / dequantize take power-of-two group sizes from 8 to 512
+    assert lib.fi_int4_quantize(16, 256, 4, 256, 96, 16, 128, 16, 2, None) == \
         _lib.FI_ERR_UNSUPPORTED
+    assert b"groupsize 96" in lib.fi_last_error()
+    assert lib.fi_int4_dequantize(16, 128, 16, 4, 4, 256, 1024, 16, 256, None) == \
+        _lib.FI_ERR_UNSUPPORTED
+    # group size 64 is accepted; here the scale rows are too short for it (4 needed)
+    assert lib.fi_int4_quantize(16, 256, 4, 256, 64, 16, 128, 16, 2, None) == \
+        _lib.FI_ERR_INVALID
     assert lib.fi_int4_dequantize(16, 128, 16, 2, 4, 100, 128, 16, 256, None) == \
         _lib.FI_ERR_INVALID
     # empty calls return before any launch

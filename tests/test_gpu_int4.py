@@ -3,6 +3,8 @@
 
 * quantize and dequantize bit-exact against the oracle (oracle/int4.py), including
   all-zero groups, subnormal scales and values near the top of fp16;
+* group sizes 8..512 besides the reference's 128: quantize / dequantize bit-exact, and the
+  matmul (on the dequantized weight) within the same bound;
 * int4_matmul with packed weights within the fp32-accumulation bound of the float64
   product on the dequantized weights, for decode-sized M (1..64, split-K) and prefill
   sizes, odd N, strided X; the speed mode (dequantized fp16 weights) within the same
@@ -187,3 +189,40 @@ def test_int4_matmul_prefill_workspace_and_errors(hip):
                             K // 128, N, 128, out.data_ptr(), N, ws.data_ptr(), need - 256,
                             _lib.stream_handle(torch.device(DEV)))
     assert rc == _lib.FI_ERR_WORKSPACE
+
+
+@pytest.mark.parametrize("gs", [8, 32, 64, 256, 512])
+def test_other_group_sizes(hip, gs):
+    # quantize / dequantize at group sizes other than the reference's 128, bit-exact against
+    # the oracle; int4_matmul and the fused norm call on such weights (dequantized first)
+    # within the fp32-accumulation bound
+    banner(f"int4 group size {gs}")
+    from fast_infer_amd import (dequantize_int4, int4_matmul, quantize_int4_groupwise, rms_norm,
+                                rms_norm_int4_matmul)
+
+    N, K = 130, 1024
+    w = _weights(gs, N, K, big=True)
+    packed, scales = quantize_int4_groupwise(torch.from_numpy(w).to(DEV), gs)
+    ep, es = OI.quantize_int4_groupwise(w, gs)
+    torch.cuda.synchronize()
+    assert scales.shape == (N, K // gs)
+    assert np.array_equal(packed.cpu().numpy(), ep)
+    assert np.array_equal(scales.cpu().numpy().view(np.uint16), es.view(np.uint16))
+    deq = dequantize_int4(packed, scales, gs)
+    ed = OI.dequantize(ep, es, gs)
+    torch.cuda.synchronize()
+    assert np.array_equal(deq.cpu().numpy().view(np.uint16), ed.view(np.uint16))
+    w = _weights(gs + 1, N, K, 0.02)
+    packed, scales = quantize_int4_groupwise(torch.from_numpy(w).to(DEV), gs)
+    w16 = dequantize_int4(packed, scales, gs).cpu().numpy()
+    for M in (1, 40, 200):
+        x = torch.randn(M, K, generator=torch.Generator().manual_seed(M)).half()
+        out = int4_matmul(x.to(DEV), (packed, scales), groupsize=gs)
+        torch.cuda.synchronize()
+        _check(out, x.numpy(), w16)
+    nw = (1.0 + 0.1 * torch.randn(K, generator=torch.Generator().manual_seed(3))).half()
+    x = torch.randn(4, K, generator=torch.Generator().manual_seed(4)).half()
+    fused = rms_norm_int4_matmul(x.to(DEV), nw.to(DEV), (packed, scales), groupsize=gs)
+    xn = rms_norm(x.to(DEV), nw.to(DEV))
+    torch.cuda.synchronize()
+    _check(fused, xn.cpu().numpy(), w16)
