@@ -32,6 +32,8 @@ constexpr float kNegBig = -1.0e30f;
 void set_error(const char* fmt, ...);
 void clear_error();
 int check_launch(const char* what);
+// Compute units of the device that runs `stream` (cached per device).
+int device_cu_count(hipStream_t stream);
 
 // ---------------------------------------------------------------------------
 // Device helpers

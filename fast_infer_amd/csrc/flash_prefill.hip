@@ -619,13 +619,9 @@ extern "C" int fi_flash_attention_fwd(const void* q, const void* k, const void* 
   // call: one head per workgroup is then faster (batch 1 x 512: 12.8 against 22.4 us;
   // batch 1 x 3072: 93 against 101 us; from two per CU up, several heads win).
   int hpw = heads_per_wg(group);
-  if (hpw > 1) {
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-        batch * num_kv_heads * (group / hpw) * q_tiles < 2 * (int64_t)cus)
-      hpw = 1;
-  }
+  if (hpw > 1 && batch * num_kv_heads * (group / hpw) * q_tiles <
+                     2 * (int64_t)device_cu_count((hipStream_t)stream))
+    hpw = 1;
   Params p;
   p.q = (const half_t*)q;
   p.k = (const half_t*)k;

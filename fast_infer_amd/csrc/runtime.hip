@@ -1,5 +1,8 @@
-// Library-wide host helpers: error strings, version, and the MFMA layout self-test.
+// Library-wide host helpers: error strings, version, the CU count per device, and the MFMA
+// layout self-test.
 #include <stdarg.h>
+
+#include <atomic>
 
 #include "common.h"
 
@@ -23,6 +26,29 @@ int check_launch(const char* what) {
     return FI_ERR_HIP;
   }
   return FI_OK;
+}
+
+// Compute units of the device that runs `stream` (the current device for the null stream),
+// queried once per device and cached.
+int device_cu_count(hipStream_t stream) {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cache[kMaxDevices];
+  int dev = -1;
+  if (stream != nullptr) {
+    hipDevice_t d;
+    if (hipStreamGetDevice(stream, &d) == hipSuccess) dev = (int)d;
+  }
+  if (dev < 0 && hipGetDevice(&dev) != hipSuccess) dev = -1;
+  if (dev >= 0 && dev < kMaxDevices) {
+    const int v = cache[dev].load(std::memory_order_relaxed);
+    if (v > 0) return v;
+  }
+  int cus = 0;
+  if (dev < 0 || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    return 256;  // MI355X
+  if (dev < kMaxDevices) cache[dev].store(cus, std::memory_order_relaxed);
+  return cus;
 }
 
 // One wave: c = mfma16x16x32(a, b, 0) with the lane-major fragments of the header.

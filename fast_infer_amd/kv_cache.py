@@ -21,7 +21,8 @@ Differences, all keyword-only or internal:
 * The allocator decides on a host copy of the table, so allocation never waits for
   the device (the reference's ``.item()`` at :60).  ``block_table`` is a device tensor
   like the reference's; the entries ``alloc_block`` fills are written into it (batched,
-  before the tensor is next handed out), never the whole table, so a caller's in-place
+  before the tensor is next handed out, through pinned memory and an asynchronous copy,
+  so the host never waits), never the whole table, so a caller's in-place
   writes to other entries persist.  Such writes are not seen by the allocator, which
   still picks the first entry it has not filled itself; assigning ``block_table``
   replaces both copies.
@@ -68,6 +69,7 @@ class KVCache:
         self._table_dev = torch.full((1, self.max_blocks_per_seq), -1, dtype=torch.int32,
                                      device=self.device)
         self._pending: list[tuple[int, int, int]] = []  # (row, entry, block) not yet on device
+        self._staging: list[tuple[torch.Tensor, torch.cuda.Event]] = []  # pinned, in flight
 
         self.free_blocks = list(range(self.num_blocks))
         self._allocated = 0
@@ -75,13 +77,27 @@ class KVCache:
 
     # -- block table ---------------------------------------------------------------
     def _flush(self) -> None:
-        """Write the entries alloc_block filled since the last flush into the device table."""
-        if self._pending:
-            rows, cols, vals = zip(*self._pending)
-            self._pending = []
-            idx = torch.tensor([rows, cols], dtype=torch.int64).to(self.device)
-            self._table_dev.index_put_((idx[0], idx[1]),
-                                       torch.tensor(vals, dtype=torch.int32).to(self.device))
+        """Write the entries alloc_block filled since the last flush into the device table.
+
+        The (row, entry, block) triples go through pinned host memory with one
+        asynchronous copy on the current stream, then a device scatter: nothing here waits
+        for the device.  Each staging buffer is kept with an event recorded after its copy
+        until that event has completed."""
+        if not self._pending:
+            return
+        host = torch.tensor(self._pending, dtype=torch.int32).t().contiguous()
+        self._pending = []
+        if self.device.type == "cuda":
+            self._staging = [(buf, ev) for buf, ev in self._staging if not ev.query()]
+            host = host.pin_memory()
+            dev = host.to(self.device, non_blocking=True)
+            ev = torch.cuda.Event()
+            ev.record(torch.cuda.current_stream(self.device))
+            self._staging.append((host, ev))
+        else:  # a host table (allocator tests without a GPU)
+            dev = host
+        idx = dev[:2].long()
+        self._table_dev.index_put_((idx[0], idx[1]), dev[2])
 
     @property
     def block_table(self) -> torch.Tensor:

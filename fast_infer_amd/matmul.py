@@ -11,6 +11,8 @@ model.py:82 and the projection after it in one call.
 
 from __future__ import annotations
 
+import warnings
+
 import torch
 
 from . import _lib
@@ -92,9 +94,24 @@ def int4_matmul(x: torch.Tensor, w, scales=None, groupsize: int = 128, *,
     return out.reshape(*lead, N)
 
 
+_warned_group_sizes: set[int] = set()
+
+
 def _other_group_size(w, groupsize: int):
-    """Packed weights whose group size is not 128 as the dequantized fp16 tensor."""
+    """Packed weights whose group size is not 128 as the dequantized fp16 tensor.
+
+    This costs every call a full dequantization: N x K fp16 written and read back, about
+    4.5 times the packed weight's bytes.  Callers with such weights should dequantize once
+    (``dequantize_int4``) and pass the fp16 weight; the first such call per group size
+    warns."""
     if isinstance(w, tuple) and groupsize != PACKED_GROUP:
+        if groupsize not in _warned_group_sizes:
+            _warned_group_sizes.add(groupsize)
+            warnings.warn(
+                f"int4_matmul: packed weights with groupsize {groupsize} are dequantized on "
+                f"every call (the packed kernels take groupsize {PACKED_GROUP}); dequantize "
+                f"once with dequantize_int4 and pass the fp16 weight instead",
+                RuntimeWarning, stacklevel=3)
         return dequantize_int4(w[0], w[1], groupsize)
     return w
 

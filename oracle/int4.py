@@ -17,9 +17,10 @@ Pinned (tests/test_int4_oracle.py): hand-packed bytes; quantize then dequantize 
 a scale step of the input (plus fp16 rounding); each group's largest |w| maps to +-7;
 scale within one fp16 rounding of amax/7; ``dequantize`` bit-exact against torch's own
 CPU ops running the reference's ``_dequant_storage`` expression; planted nibble-order and
-sign-extension mistakes fail.  The reciprocal-multiply step of the scale cannot be run
-against CUDA here: parity unpinned for that one rounding (it differs from a true
-division in under 0.1% of groups; measured in the tests).
+sign-extension mistakes fail.  The scale's reciprocal multiply and a true division give
+the same fp16 scale for every possible fp16 ``w_max`` (checked exhaustively), and the GPU
+tests compare the quantizer bit for bit with the reference's expression run by torch on
+the device itself.
 """
 
 from __future__ import annotations

@@ -48,20 +48,64 @@ def test_paged_decode_head_dim(hip, D, lens):
     assert _maxabs(out, OA.paged_attention(q, kc, vc, table, 64, lens)) <= ATOL
 
 
-def test_paged_decode_head_dim_64_strided_output_untouched(hip):
-    # q and o as views of wider rows: the columns past head_dim keep their bytes
-    banner("paged decode head_dim 64, strided q/o")
-    from fast_infer_amd import paged_attention
+_SENTINEL = 0x7C01  # an fp16 NaN bit pattern no kernel produces
 
-    sp = dict(B=2, Hq=8, Hkv=2, D=64, bs=64, N=32, lens=[700, 90], seed=5)
+
+@pytest.mark.parametrize("lens", [[300, 90], [700, 90]])
+def test_paged_decode_head_dim_64_leaves_bytes_past_head_dim(hip, lens):
+    # fi_paged_attention_fwd through the C ABI with q and o as views of 128-wide rows: the
+    # single-pass kernel (rows within one partition) and the partition + merge launches
+    # write the 64 columns of each head and nothing past them
+    banner(f"paged decode head_dim 64, C ABI, o columns 64..127 untouched, lens {lens}")
+    from fast_infer_amd import _lib
+
+    sp = dict(B=2, Hq=8, Hkv=2, D=64, bs=64, N=32, lens=lens, seed=5)
     q, kc, vc, table, lens = specs.decode_inputs(sp)
-    qw = torch.zeros(2, 8, 128, dtype=torch.float16)
-    qw[..., :64] = q
-    qd = qw.to(DEV)[..., :64]
-    out = paged_attention(qd, kc.to(DEV), vc.to(DEV), table.to(DEV), 64, 700,
-                          context_lens=torch.tensor(lens, dtype=torch.int32, device=DEV))
+    qw = torch.zeros(2, 8, 128, dtype=torch.float16, device=DEV)
+    qw[..., :64] = q.to(DEV)
+    ow = torch.full((2, 8, 128), 0, dtype=torch.int16, device=DEV).fill_(_SENTINEL)
+    ow = ow.view(torch.float16)
+    kcd, vcd, td = kc.to(DEV), vc.to(DEV), table.to(DEV)
+    cl = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    lib = _lib.load()
+    nbytes = lib.fi_paged_attention_workspace_size(2, 8, 2, max(lens), 64)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=DEV)
+    rc = lib.fi_paged_attention_fwd(
+        qw.data_ptr(), qw.stride(0), qw.stride(1), kcd.data_ptr(), vcd.data_ptr(), 32, 64, 2,
+        td.data_ptr(), td.stride(0), td.shape[1], cl.data_ptr(), max(lens),
+        ow.data_ptr(), ow.stride(0), ow.stride(1), 2, 8, 64, 64 ** -0.5,
+        ws.data_ptr() if nbytes else None, nbytes, _lib.stream_handle(torch.device(DEV)))
+    _lib.check(rc, "paged_attention")
     torch.cuda.synchronize()
-    assert _maxabs(out, OA.paged_attention(q, kc, vc, table, 64, lens)) <= ATOL
+    assert torch.all(ow.view(torch.int16)[..., 64:] == _SENTINEL)
+    assert _maxabs(ow[..., :64], OA.paged_attention(q, kc, vc, table, 64, lens)) <= ATOL
+
+
+@pytest.mark.parametrize("S", [70, 300])
+def test_flash_prefill_head_dim_64_leaves_bytes_past_head_dim(hip, S):
+    # fi_flash_attention_fwd through the C ABI with o a view of 128-wide rows
+    banner(f"flash prefill head_dim 64, C ABI, o columns 64..127 untouched, S={S}")
+    from fast_infer_amd import _lib
+
+    B, H, Hkv, D = 2, 6, 2, 64
+    g = torch.Generator().manual_seed(S)
+    q = torch.randn(B, S, H, D, generator=g).half()
+    k = torch.randn(B, S, Hkv, D, generator=g).half()
+    v = torch.randn(B, S, Hkv, D, generator=g).half()
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    ow = torch.empty(B, S, H, 128, dtype=torch.int16, device=DEV).fill_(_SENTINEL)
+    ow = ow.view(torch.float16)
+    lib = _lib.load()
+    rc = lib.fi_flash_attention_fwd(
+        qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), ow.data_ptr(), B, H, Hkv, S, D,
+        qd.stride(0), qd.stride(2), qd.stride(1), kd.stride(0), kd.stride(2), kd.stride(1),
+        vd.stride(0), vd.stride(2), vd.stride(1), ow.stride(0), ow.stride(2), ow.stride(1),
+        D ** -0.5, None, None, 0, 64, None, 0, 0, _lib.stream_handle(torch.device(DEV)))
+    _lib.check(rc, "flash_attention")
+    torch.cuda.synchronize()
+    assert torch.all(ow.view(torch.int16)[..., 64:] == _SENTINEL)
+    ref = OA.causal_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2))
+    assert _maxabs(ow[..., :64].transpose(1, 2), ref) <= ATOL
 
 
 @pytest.mark.parametrize("D", [64, 96])

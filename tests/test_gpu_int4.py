@@ -3,6 +3,8 @@
 
 * quantize and dequantize bit-exact against the oracle (oracle/int4.py), including
   all-zero groups, subnormal scales and values near the top of fp16;
+* quantize bit-exact against the reference's own expression (loader.py:20-38) evaluated by
+  torch on the same GPU, over groups whose maxima cover every positive fp16 value;
 * group sizes 8..512 besides the reference's 128: quantize / dequantize bit-exact, and the
   matmul (on the dequantized weight) within the same bound;
 * int4_matmul with packed weights within the fp32-accumulation bound of the float64
@@ -50,6 +52,49 @@ def test_quantize_dequantize_bitexact(hip, N, K):
     ed = OI.dequantize(ep, es)
     torch.cuda.synchronize()
     assert np.array_equal(deq.cpu().numpy().view(np.uint16), ed.view(np.uint16))
+
+
+def _reference_quantize_on_device(w: torch.Tensor, groupsize: int = 128):
+    """loader.py:20-38 run as torch tensor ops on the GPU: the reference's own arithmetic
+    (``w_max / 7.0`` on a device tensor, ``torch.round(w / scale)``) on the same device."""
+    out_features, in_features = w.shape
+    w = w.reshape(out_features, -1, groupsize)
+    w_max = torch.clamp(w.abs().amax(dim=-1, keepdim=True), min=1e-6)
+    scale = w_max / 7.0
+    w_q = torch.clamp(torch.round(w / scale.to(w.dtype)), -8, 7).to(torch.int8)
+    w_q = w_q.reshape(out_features, -1, groupsize // 2, 2)
+    packed = ((w_q[..., 0] & 0xF) | ((w_q[..., 1] & 0xF) << 4))
+    packed = packed.reshape(out_features, in_features // 2).to(torch.int8)
+    return packed, scale.reshape(out_features, in_features // groupsize).to(torch.float16)
+
+
+@pytest.mark.parametrize("N,K", [(5120, 3072), (7, 1024)])
+def test_quantize_matches_reference_expression_on_device(hip, N, K):
+    """fi_int4_quantize against the reference's expression evaluated by torch on this GPU,
+    bit for bit: random weights, an all-zero group (clamped to fp16(1e-6)), subnormal
+    scales, values near the top of fp16, and one group per row whose maximum walks through
+    every positive finite fp16 value in turn (so every possible scale is produced)."""
+    banner(f"int4 quantize vs the reference expression on the GPU, N={N} K={K}")
+    from fast_infer_amd import quantize_int4_groupwise
+
+    w = _weights(N * 7 + K, N, K, big=True)
+    every = np.arange(1, 0x7C00, dtype=np.uint16).view(np.float16)  # all positive finite fp16
+    groups = N * (K // 128)
+    maxima = np.resize(every, groups).reshape(N, K // 128)
+    g = w.reshape(N, K // 128, 128).astype(np.float32)
+    g = np.clip(g, -np.abs(maxima[..., None]).astype(np.float32), np.abs(maxima[..., None]))
+    g[..., 5] = maxima  # each group's largest |w| is exactly this value
+    g[..., 6] = -maxima * np.float16(0.5)
+    w = g.reshape(N, K).astype(np.float16)
+    wd = torch.from_numpy(w).to(DEV)
+    packed, scales = quantize_int4_groupwise(wd)
+    rp, rs = _reference_quantize_on_device(wd)
+    torch.cuda.synchronize()
+    assert torch.equal(scales.view(torch.int16), rs.view(torch.int16))
+    assert torch.equal(packed, rp)
+    ep, es = OI.quantize_int4_groupwise(w)
+    assert np.array_equal(packed.cpu().numpy(), ep)
+    assert np.array_equal(scales.cpu().numpy().view(np.uint16), es.view(np.uint16))
 
 
 def _check(out, x, w16):
@@ -191,6 +236,7 @@ def test_int4_matmul_prefill_workspace_and_errors(hip):
     assert rc == _lib.FI_ERR_WORKSPACE
 
 
+@pytest.mark.filterwarnings("ignore:int4_matmul. packed weights with groupsize")
 @pytest.mark.parametrize("gs", [8, 32, 64, 256, 512])
 def test_other_group_sizes(hip, gs):
     # quantize / dequantize at group sizes other than the reference's 128, bit-exact against

@@ -89,8 +89,8 @@ def test_dequantize_matches_torch_cpu_ops():
 
 def test_quantize_matches_torch_cpu_ops():
     """loader.py:20-38's expressions run by torch on the CPU, where ``w_max / 7.0`` is a
-    true fp32 division: bit-exact with the oracle's ``true_division`` form.  The CUDA
-    form multiplies by the fp32 reciprocal; the two scales differ in few groups."""
+    true fp32 division: bit-exact with the oracle's ``true_division`` form, and with the
+    reciprocal form the device uses (the two agree on every fp16 input, below)."""
     rng = np.random.default_rng(2)
     w = _weights(rng, 256, 1024)
     wt = torch.from_numpy(w).reshape(256, -1, 128)
@@ -103,8 +103,24 @@ def test_quantize_matches_torch_cpu_ops():
     assert np.array_equal(p_div, packed_t.numpy())
     assert np.array_equal(s_div.view(np.uint16), scale.reshape(256, 8).numpy().view(np.uint16))
     p_rec, s_rec = OI.quantize_int4_groupwise(w)
-    differ = np.mean(s_rec != s_div)
-    assert differ < 0.01, differ   # the reciprocal form: same scale in > 99% of groups
+    assert np.array_equal(p_rec, p_div) and np.array_equal(s_rec.view(np.uint16), s_div.view(np.uint16))
+
+
+def test_scale_reciprocal_and_division_agree_on_every_fp16():
+    """``w_max / 7.0`` on a device tensor multiplies by the fp32 reciprocal of 7; on the CPU
+    it divides.  Over every positive finite fp16 ``w_max`` (and the clamp value fp16(1e-6))
+    both give the same fp16 scale, so the scale step is pinned whichever form runs."""
+    h = np.arange(1, 0x7C00, dtype=np.uint16).view(np.float16)
+    a = np.maximum(h.astype(np.float32), np.float32(np.float16(1e-6)))
+    rec = (a * (np.float32(1.0) / np.float32(7.0))).astype(np.float16)
+    div = (a / np.float32(7.0)).astype(np.float16)
+    assert np.array_equal(rec.view(np.uint16), div.view(np.uint16))
+    # the oracle's two forms agree on the same inputs
+    w = np.zeros((h.size // 128, 128), np.float16)
+    w[:, 0] = h[: w.shape[0] * 128].reshape(-1, 128)[:, -1]
+    _, s_rec = OI.quantize_int4_groupwise(w)
+    _, s_div = OI.quantize_int4_groupwise(w, true_division=True)
+    assert np.array_equal(s_rec.view(np.uint16), s_div.view(np.uint16))
 
 
 @pytest.mark.parametrize("seed", [3, 4])
