@@ -20,7 +20,9 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <type_traits>
 #include <mutex>
+#include <vector>
 
 #include "common.h"
 
@@ -48,6 +50,10 @@ struct Params {
   int groups_per_split;
   const half_t* norm_w;  // RMSNorm weight [K] when the norm is fused into the X operand
   float eps;
+  // gemm_sk_kernel: column tiles, K splits and the per-tile arrival counters
+  int tiles;
+  int ksplit;
+  unsigned* counters;
 };
 
 __device__ __forceinline__ uint32_t as_u32(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
@@ -320,208 +326,361 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(Params p) {
 }
 
 // ---------------------------------------------------------------------------------------
-// Packed-weight GEMM for 17..64 rows, staged through direct-to-LDS copies.  A workgroup
-// computes a 64-column x MT-row tile over a slice of the K groups with eight waves: wave
-// w = 4h + q takes columns 16q .. +15 of the groups t with t % 2 == h, so the SIMD's two
-// waves overlap one group's dequantization, LDS reads and MFMAs with the other's; the two
-// halves' sums are added through LDS at the end.  Each group's X tile (MT rows x 256
-// bytes) and W tile (64 rows x 64 bytes) are copied global -> LDS with `buffer_load ...
-// lds` into a ring of kDmaStages pairs of groups, two pairs ahead of the MFMAs; the copies
-// hold no registers.
+// Packed-weight GEMM for 17..64 rows with the K split added up in the same launch.
 //
-// X rows sit in LDS unpadded, their 16-byte chunks XOR-permuted by row % 16 (the copy
-// lane that fills slot c of row r fetches chunk c ^ (r % 16)), so the 16 rows one MFMA
-// operand read touches fall on distinct banks.  X rows past M and weight rows past N read
-// zeros through the buffer bounds check.  The group scales of the workgroup's 64 columns
-// are staged in LDS once, at the start.
-constexpr int kDmaThreads = 512;
-constexpr int kDmaStages = 3;      // pairs of groups in the ring
-constexpr int kDmaMaxGroups = 64;  // K groups per workgroup (one K split) the scale table holds
+// A workgroup of eight multiplying waves and four loading waves computes a 64-column x MT-row
+// tile over a slice of G <= 8 K groups.  Multiplying wave w = 4h + q takes output columns
+// 32h .. 32h + 31 (column half h) and the q-th quarter of each phase's k-steps (32 k each),
+// so the two waves of a SIMD (w and w + 4) read the same X fragments for different weights,
+// and each weight is unpacked once.  Within a wave the next k-step's unpack is interleaved
+// with the current k-step's MFMAs.  X fragments are read from LDS once per 32 output columns.
+//
+// The loading waves copy the slice's X tiles (MT rows x 256 bytes per group, 16-byte chunks
+// XOR-permuted by row % 16) and W tiles (64 columns x 64 bytes per group, 16-byte chunks
+// XOR-permuted by (column / 2) % 4) global -> LDS with `buffer_load ... lds`, in two phases
+// (the first ceil(G / 2) groups, then the rest while the first phase is multiplied), so that
+// a full memory queue stalls only those waves.  The multiplying waves load only the scales
+// of their columns.  The four quarters' sums of each column half are then added through LDS
+// in quarter order.
+//
+// K split: the workgroups of one column tile have block ids congruent modulo 8, which the
+// dispatcher places on one XCD (checked once per device before this kernel is used), so a
+// tile's partial sums and its arrival counter are shared through that XCD's L2.  Each
+// workgroup stores its partial tile, waits until the stores are done, and increments the
+// tile's counter; the workgroup that arrives last loads the other partials (bypassing L1),
+// adds all of them in split order (the same sum whichever workgroup is last), writes the
+// fp16 tile and sets the counter back to zero for the next call.  No workgroup waits for
+// another.  Block id b: XCD group b % 8, split (b / 8) / T8, tile 8 * ((b / 8) % T8) + b % 8,
+// with T8 = ceil(tiles / 8).
+constexpr int kSkWaves = 8;                         // multiplying waves
+constexpr int kSkLoaders = 4;                       // loading waves
+constexpr int kSkMaxGroups = 8;                     // K groups per workgroup
+constexpr int kSkTilesPerXcd = 256;                 // counters per XCD group and stream
+constexpr int kSkMaxTiles = 8 * kSkTilesPerXcd;     // column tiles per call
+constexpr int kSkStreamSlots = 16;                  // streams per device with their own counters
 
 template <int MT>
-struct DmaTile {
-  static constexpr int kXBytes = MT * 256;     // X tile of one group
-  static constexpr int kWBytes = kNTile * 64;  // W tile of one group (4 KiB)
-  static constexpr int kStage = kXBytes + kWBytes;
-  static constexpr int kPair = 2 * kStage;
-  static constexpr int kCopies = kStage / 1024;  // 1 KiB copies per group: MT / 4 of X, 4 of W
-  static constexpr int kIssue = kCopies / 4;     // copies per wave per pair
-  static_assert(kCopies % 4 == 0, "the four waves of a half share a group's copies evenly");
-  // workgroups per CU the ring and scale table leave room for in 160 KiB of LDS
-  static constexpr int kLds = kDmaStages * kPair + kNTile * kDmaMaxGroups * 2;
-  static constexpr int kMinBlocks = 160 * 1024 / kLds >= 2 ? 2 : 1;
+struct SkTile {
+  static constexpr int kX = MT * 256;              // X tile of one group
+  static constexpr int kW = kNTile * 64;           // W tile of one group
+  static constexpr int kSlot = kX + kW;
+  static constexpr int kXCopies = MT / 4;          // 1 KiB copies of 4 X rows
+  static constexpr int kCopies = kXCopies + 4;     // + 4 of 16 W columns
+  static constexpr int kMSub = MT / 16;            // 16-row blocks
+  static constexpr int kBlocks = 4 * kMSub;        // 16 x 16 output blocks
+  static constexpr int kOwn = kBlocks / kSkWaves;  // blocks each wave finishes
+  static constexpr int kLds = kSkMaxGroups * kSlot;
+  static_assert(kLds <= 160 * 1024, "the slots fit one CU's LDS");
+  static_assert(kBlocks * 4 * 1024 + 16 <= kLds, "the reduction area fits the slots");
+  static_assert(kOwn >= 1 && kBlocks % kSkWaves == 0, "whole blocks per wave");
 };
 
-// The copies of one wave for the group pair it serves: copies (w % 4) * kIssue + i of its
-// half's group, X slots first (rows 4c .. 4c + 3 of slot c), then W slots (rows 16c .. +15).
-template <int MT>
-struct DmaCopies {
-  int voff[DmaTile<MT>::kIssue];  // per lane: byte offset in X or W at group 0
-  int lds[DmaTile<MT>::kIssue];   // byte offset of the copy in a group's stage
-  bool is_x[DmaTile<MT>::kIssue];
-};
-
-template <int MT>
-__device__ __forceinline__ DmaCopies<MT> dma_copies(const Params& p, int wave, int lane) {
-  using T = DmaTile<MT>;
-  DmaCopies<MT> c;
+// fp16 store of C[m][nb .. nb + 3] (columns past N dropped)
+__device__ __forceinline__ void store_half4(const Params& p, floatx4 v, int m, int nb) {
+  half_t* dst = p.out + (int64_t)m * p.out_stride + nb;
+  const half4 h = to_half4(v);
+  if (nb + 3 < p.N && ((uintptr_t)dst & 7) == 0) {
+    *(half4*)dst = h;
+  } else {
 #pragma unroll
-  for (int i = 0; i < T::kIssue; ++i) {
-    const int ci = (wave & 3) * T::kIssue + i;
-    c.is_x[i] = ci < MT / 4;
-    if (c.is_x[i]) {
-      const int r = 4 * ci + (lane >> 4);
-      c.voff[i] = r * (int)p.x_stride * 2 + (((lane & 15) ^ (r & 15)) << 4);
-      c.lds[i] = ci * 1024;
-    } else {
-      const int wi = ci - MT / 4;
-      c.voff[i] = (16 * wi + (lane >> 2)) * (int)p.w_stride + (lane & 3) * 16;
-      c.lds[i] = T::kXBytes + wi * 1024;
-    }
-  }
-  return c;
-}
-
-// This wave's copies of group g into the group's stage.
-template <int MT>
-__device__ __forceinline__ void dma_issue(rsrc_t xr, rsrc_t wr, char* stage, int g,
-                                          const DmaCopies<MT>& c) {
-  using T = DmaTile<MT>;
-  const uint32_t base = lds_addr(stage);
-#pragma unroll
-  for (int i = 0; i < T::kIssue; ++i) {
-    if (c.is_x[i])
-      lds_copy16(xr, base + c.lds[i], c.voff[i], g * 256);
-    else
-      lds_copy16(wr, base + c.lds[i], c.voff[i], g * (kGroup / 2));
+    for (int i = 0; i < 4; ++i)
+      if (nb + i < p.N) dst[i] = h[i];
   }
 }
 
-// One group's MFMAs from a resident stage: this lane's 16 weight bytes (k = 32 grp ..
-// +31 of column 16 q + row) dequantized with the group's scale, against X rows 16 j + row.
-template <int MT>
-__device__ __forceinline__ void dma_group(const char* stage, const half_t* sc, int t, int q,
-                                          int row, int grp, floatx4 (&acc)[MT / 16]) {
-  using T = DmaTile<MT>;
-  const u32x4 wv = *(const u32x4*)(stage + T::kXBytes + q * 1024 + row * 64 + grp * 16);
-  const half_t s = sc[(16 * q + row) * kDmaMaxGroups + t];
-  // every X fragment read goes out before the dequantization and the MFMAs, so one LDS
-  // latency covers them all
-  u32x4 xv[4][MT / 16];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int chunk = ((4 * grp + k) ^ row) << 4;
-#pragma unroll
-    for (int j = 0; j < MT / 16; ++j)
-      xv[k][j] = *(const u32x4*)(stage + (16 * j + row) * 256 + chunk);
-  }
-  __builtin_amdgcn_sched_barrier(0);
-  const half2_t s2 = {s, s};
-  half8 wf[4];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) wf[k] = dequant8(wv[k], s2);
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-#pragma unroll
-    for (int j = 0; j < MT / 16; ++j) acc[j] = mfma16x16x32(wf[k], as_half8(xv[k][j]), acc[j]);
-  }
+// dequant8 with each mask-and-insert as one v_and_or_b32 (the mask from a scalar register,
+// the fp16 exponent bits from a vector register): 18 VALU instructions per eight weights,
+// the same values bit for bit.
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t bits) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(mask), "v"(bits));
+  return r;
+}
+
+__device__ __forceinline__ half8 dequant8_ao(uint32_t d, half2_t s2, uint32_t mask, uint32_t bits) {
+#pragma clang fp contract(off)
+  d ^= 0x88888888u;
+  const uint32_t e = d >> 4;
+  const uint32_t lo = __builtin_amdgcn_perm(e, d, 0x05040100u);
+  const uint32_t hi = __builtin_amdgcn_perm(e, d, 0x07060302u);
+  const half2_t bias = {(half_t)1032.0f, (half_t)1032.0f};
+  u32x4 r;
+  r[0] = as_u32((as_h2(and_or(lo, mask, bits)) - bias) * s2);
+  r[1] = as_u32((as_h2(and_or(lo >> 8, mask, bits)) - bias) * s2);
+  r[2] = as_u32((as_h2(and_or(hi, mask, bits)) - bias) * s2);
+  r[3] = as_u32((as_h2(and_or(hi >> 8, mask, bits)) - bias) * s2);
+  return as_half8(r);
 }
 
 template <int MT>
-__global__ __launch_bounds__(kDmaThreads, DmaTile<MT>::kMinBlocks) void gemm_dma_kernel(Params p) {
-  using T = DmaTile<MT>;
-  constexpr int kMSub = MT / 16;
-  constexpr int S = kDmaStages;
-  static_assert(S >= 2 && S <= 3, "the step loop's wait covers 0..1 pairs ahead");
-  __shared__ __attribute__((aligned(16))) char ring[S * T::kPair];
-  __shared__ half_t sc[kNTile * kDmaMaxGroups];
+__global__ __launch_bounds__((kSkWaves + kSkLoaders) * 64, 1) void gemm_sk_kernel(Params p) {
+  using T = SkTile<MT>;
+  constexpr int kMSub = T::kMSub;
+  __shared__ __attribute__((aligned(16))) char lds[T::kLds];
+
+  const int t8 = (p.tiles + 7) >> 3;
+  const int xg = blockIdx.x & 7, kk = blockIdx.x >> 3;
+  const int s = kk / t8;
+  const int t = 8 * (kk - s * t8) + xg;
+  if (t >= p.tiles) return;  // padding of the last XCD group (uniform, before any barrier)
 
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int h = wave >> 2;  // which group of each pair
-  const int q = wave & 3;   // which 16 columns
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const bool producer = w >= kSkWaves;
+  const int l = w - kSkWaves;  // loading wave index
+  const int h = (w >> 2) & 1;  // column half
+  const int q = w & 3;         // k-step of every group
   const int row = lane & 15;
   const int grp = lane >> 4;
-  const int n0 = blockIdx.x * kNTile;
-  const int m0 = blockIdx.y * MT;
+  const int n0 = t * kNTile;
   const int groups = p.K / kGroup;
-  const int g_begin = blockIdx.z * p.groups_per_split;
-  const int G = min(g_begin + p.groups_per_split, groups) - g_begin;  // <= 0: nothing to add
-  const int P = (G + 1) / 2;                                          // group pairs
+  const int g_begin = s * p.groups_per_split;
+  const int G = min(p.groups_per_split, groups - g_begin);  // 1 .. 8 (host plan)
+  const int GA = (G + 1) >> 1;                               // groups of phase A
+  const int GB = G - GA;                                     // of phase B
 
-  const int rows_x = min(MT, p.M - m0);
-  const int rows_w = min(kNTile, p.N - n0);
-  const rsrc_t xr =
-      raw_rsrc(p.x + (int64_t)m0 * p.x_stride, (int)((rows_x - 1) * p.x_stride * 2 + p.K * 2));
-  const rsrc_t wr = raw_rsrc(p.w + (int64_t)n0 * p.w_stride, (int)((rows_w - 1) * p.w_stride + p.K / 2));
-  const DmaCopies<MT> cp = dma_copies<MT>(p, wave, lane);
-
-  // The first S - 1 pairs' copies go out before the scale table is read, so the two
-  // latencies overlap.  The compiler waits for the scale loads (and with them for every
-  // copy issued before them) before writing the table; step 0's barrier publishes it.
-  // A pair's second group past the split (odd G) is copied like the others (the buffer
-  // bounds keep it in range) and never multiplied.
+  floatx4 acc[2][kMSub];
 #pragma unroll
-  for (int u = 0; u < S - 1; ++u)
-    if (u < P) dma_issue<MT>(xr, wr, ring + u * T::kPair + h * T::kStage, g_begin + 2 * u + h, cp);
-  for (int f = threadIdx.x; f < kNTile * G; f += kDmaThreads) {
-    const int col = f / G, t = f - col * G;
-    const int n = min(n0 + col, p.N - 1);
-    sc[col * kDmaMaxGroups + t] = p.scales[(int64_t)n * p.s_stride + g_begin + t];
-  }
-
-  floatx4 acc[kMSub];
+  for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
-  for (int j = 0; j < kMSub; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < kMSub; ++i) acc[jj][i] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  // Step u: wait for this wave's copies of pair u (the pair after it may still be in
-  // flight), barrier (every wave's copies of pair u have landed, every wave is done with
-  // pair u - 1's stage), refill that stage with pair u + S - 1, multiply this half's group.
-  for (int u = 0; u < P; ++u) {
-    if (u + 1 < P && S > 2)
-      wait_vmcnt<T::kIssue>();
-    else
+  if (producer) {
+    // X rows past M and weight rows past N read zeros through the buffer bounds
+    const rsrc_t xr = raw_rsrc(p.x, (int)((min(MT, p.M) - 1) * p.x_stride * 2 + p.K * 2));
+    const rsrc_t wr = raw_rsrc(p.w + (int64_t)n0 * p.w_stride,
+                              (int)((min(kNTile, p.N - n0) - 1) * p.w_stride + p.K / 2));
+    // copy cc of a group: X rows 4cc .. 4cc + 3 (row 4cc + lane / 16, slot lane % 16 <- chunk
+    // slot ^ (row % 16)), then W columns 16cw .. 16cw + 15 (column 16cw + lane / 4, slot
+    // lane % 4 <- 16-byte chunk slot ^ ((column / 2) % 4), so that the weight reads of eight
+    // consecutive columns fall on distinct banks).  Loading wave l issues X copies cc = l,
+    // l + 4, ... and W copy cw = l of every group; per-lane offsets at group 0.
+    constexpr int kXPer = T::kXCopies / kSkLoaders;
+    static_assert(T::kXCopies % kSkLoaders == 0, "X copies split evenly over the loading waves");
+    int xoff[kXPer];
+#pragma unroll
+    for (int i = 0; i < kXPer; ++i) {
+      const int r = 4 * (l + kSkLoaders * i) + (lane >> 4);
+      xoff[i] = r * (int)p.x_stride * 2 + (((lane & 15) ^ (r & 15)) << 4);
+    }
+    const int woff = (16 * l + (lane >> 2)) * (int)p.w_stride + (((lane & 3) ^ ((lane >> 3) & 3)) << 4);
+    auto issue = [&](int u0, int gp) {
+#pragma unroll 1
+      for (int u = u0; u < u0 + gp; ++u) {
+        const uint32_t base = lds_addr(lds + u * T::kSlot);
+        const int g = g_begin + u;
+#pragma unroll
+        for (int i = 0; i < kXPer; ++i)
+          lds_copy16(xr, base + (l + kSkLoaders * i) * 1024, xoff[i], g * 256);
+        lds_copy16(wr, base + T::kX + l * 1024, woff, g * (kGroup / 2));
+      }
+    };
+    // phase A, then phase B while the other waves multiply phase A
+    issue(0, GA);
+    wait_vmcnt<0>();
+    asm volatile("s_barrier" ::: "memory");
+    if (GB > 0) {
+      issue(GA, GB);
       wait_vmcnt<0>();
-    wait_lgkmcnt0();  // the scale table's LDS writes (step 0)
-    __builtin_amdgcn_s_barrier();
-    if (u + S - 1 < P)
-      dma_issue<MT>(xr, wr, ring + ((u + S - 1) % S) * T::kPair + h * T::kStage,
-                    g_begin + 2 * (u + S - 1) + h, cp);
-    if (2 * u + h < G)
-      dma_group<MT>(ring + (u % S) * T::kPair + h * T::kStage, sc, 2 * u + h, q, row, grp, acc);
-  }
+      asm volatile("s_barrier" ::: "memory");
+    }
+  } else {
+    // Wave (h, q) multiplies the q-th quarter of each phase's k-steps (a k-step is 32 k of one
+    // group: lane group grp supplies k = 32 grp + 8k .. +7, weight dword k of the lane's 16
+    // bytes and X chunk 4 grp + k) for its two column blocks j = 2h, 2h + 1.  In a phase of gp
+    // groups from u0 these are k-steps q gp .. q gp + gp - 1, in group u0 + (q gp) / 4 and
+    // possibly the next one (the same group for all four when gp = 4).  The scales of the
+    // lane's columns (16j + row; past N the last column, times zero weights) for those two
+    // groups: sv[jj][second].  These are the only memory loads of these waves, so the
+    // compiler's own wait before their first use waits for nothing else.
+    struct Scales {  // bits of sv[jj][0] in the low half, sv[jj][1] in the high half
+      uint32_t v0, v1;
+    };
+    auto load_scales = [&](int u0, int gp) {
+      const int uf = u0 + (q * gp) / 4;
+      const int us = min(uf + 1, G - 1);
+      uint32_t v[2];
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const uint16_t* sp = (const uint16_t*)p.scales +
+                             (int64_t)min(n0 + 16 * (2 * h + jj) + row, p.N - 1) * p.s_stride + g_begin;
+        v[jj] = (uint32_t)sp[uf] | ((uint32_t)sp[us] << 16);
+      }
+      return Scales{v[0], v[1]};
+    };
+    const Scales sca = load_scales(0, GA);
+    const Scales scb = GB > 0 ? load_scales(GA, GB) : sca;
+    const uint32_t mask = __builtin_amdgcn_readfirstlane(0x000F000Fu);
+    const uint32_t bits = 0x64006400u;
 
-  // the second half's sums join the first half's through the (now idle) ring
-  floatx4* red = (floatx4*)ring;
-  __syncthreads();
-  if (h == 1) {
+    // One phase, software pipelined: k-step i + 2's fragments are read and k-step i + 1's
+    // weights unpacked while k-step i's MFMAs run.
+    auto run_phase = [&](int u0, int gp, const Scales sv) {
+      const int ks0 = q * gp;
+      const int uf = u0 + ks0 / 4;
+      u32x4 xv[3][kMSub];
+      uint32_t wd[3][2];
+      bool sec[3];
+      half8 wf[2][2];
+      auto read = [&](int b, int i) {  // k-step ks0 + i
+        const int ks = ks0 + i;
+        const int u = u0 + ks / 4, k = ks & 3;
+        const char* slot = lds + u * T::kSlot;
 #pragma unroll
-    for (int j = 0; j < kMSub; ++j) red[(q * kMSub + j) * 64 + lane] = acc[j];
-  }
-  __syncthreads();
-  // The finished tile is staged after the reduction area, rows padded to 272 bytes, and
-  // written out row by row: 16 consecutive lanes store one row's 64 columns, where each
-  // lane's own accumulators would give 64-byte pieces of 16 rows (the workgroup's slot is
-  // held until its last stores complete).
-  constexpr int kTRow = 272;
-  char* tile = ring + 4 * kMSub * 64 * (int)sizeof(floatx4);
-  static_assert(4 * kMSub * 64 * sizeof(floatx4) + MT * kTRow <= S * T::kPair,
-                "the staged tile fits the ring");
-  static_assert(MT * 16 % kDmaThreads == 0, "whole rounds of row pieces");
-  if (h == 0) {
+        for (int ii = 0; ii < kMSub; ++ii)
+          xv[b][ii] = *(const u32x4*)(slot + (16 * ii + row) * 256 + (((4 * grp + k) ^ row) << 4));
 #pragma unroll
-    for (int j = 0; j < kMSub; ++j) {
-      acc[j] += red[(q * kMSub + j) * 64 + lane];
-      *(floatx4*)(tile + (16 * j + row) * kTRow + (16 * q + 4 * grp) * 4) = acc[j];
+        for (int jj = 0; jj < 2; ++jj)
+          wd[b][jj] = *(const uint32_t*)(slot + T::kX + (16 * (2 * h + jj) + row) * 64 +
+                                         ((grp ^ ((row >> 1) & 3)) << 4) + 4 * k);
+        sec[b] = u != uf;
+      };
+      auto unpack = [&](int b, int i) {
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+          const uint32_t both = jj ? sv.v1 : sv.v0;
+          const half_t sc = __builtin_bit_cast(half_t, (uint16_t)(both >> (sec[b] ? 16 : 0)));
+          wf[i & 1][jj] = dequant8_ao(wd[b][jj], half2_t{sc, sc}, mask, bits);
+        }
+      };
+      read(0, 0);
+      read(1, min(1, gp - 1));
+      unpack(0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (i < gp) {  // uniform
+          if (i + 2 < gp) read((i + 2) % 3, i + 2);
+          // k-step i + 1's unpack (unused past the phase) between k-step i's MFMAs
+          if (i < 3) unpack((i + 1) % 3, i + 1);
+#pragma unroll
+          for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+            for (int ii = 0; ii < kMSub; ++ii) {
+              acc[jj][ii] = mfma16x16x32(wf[i & 1][jj], as_half8(xv[i % 3][ii]), acc[jj][ii]);
+              if (i < 3) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, 36 / (2 * kMSub), 0);  // then VALU
+              }
+            }
+        }
+      }
+    };
+
+    asm volatile("s_barrier" ::: "memory");  // phase A has landed
+    run_phase(0, GA, sca);
+    if (GB > 0) {
+      asm volatile("s_barrier" ::: "memory");  // phase B has landed
+      run_phase(GA, GB, scb);
     }
   }
-  __syncthreads();
-  const int rows = min(MT, p.M - m0);
+
+  // The quarters' sums, added in quarter order through the (now idle) slots: block b = 4 i + j
+  // of quarter q at red[(b * 4 + q) * 64 + lane]; wave (h, q) finishes blocks 2 i + jj = q * kOwn
+  // .. + kOwn - 1 of its half.  The loading waves only take part in the barriers.
+  floatx4* red = (floatx4*)lds;
+  __syncthreads();  // every wave is done with the slots
+  if (!producer) {
 #pragma unroll
-  for (int it = 0; it < MT * 16 / kDmaThreads; ++it) {
-    const int idx = threadIdx.x + kDmaThreads * it;
-    const int r = idx >> 4, c = idx & 15;
-    if (r < rows) store_row_piece(p, *(const floatx4*)(tile + r * kTRow + 16 * c), m0 + r, n0 + 4 * c);
+    for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+      for (int i = 0; i < kMSub; ++i)
+        red[((4 * i + 2 * h + jj) * 4 + q) * 64 + lane] = acc[jj][i];
+  }
+  __syncthreads();
+  floatx4 v[T::kOwn];
+  int ob[T::kOwn];  // block index (4 i + j) of each finished block
+#pragma unroll
+  for (int o = 0; o < T::kOwn; ++o) {
+    const int hb = q * T::kOwn + o;  // block within the half: 2 i + jj
+    const int b = 4 * (hb >> 1) + 2 * h + (hb & 1);
+    ob[o] = b;
+    v[o] = red[(b * 4) * 64 + lane];
+#pragma unroll
+    for (int qq = 1; qq < 4; ++qq) v[o] += red[(b * 4 + qq) * 64 + lane];
+  }
+
+  if (p.ksplit > 1) {
+    // partial tile of (t, s): block b at [b][lane], 1 KiB per block
+    floatx4* part = (floatx4*)p.partial + (int64_t)t * p.ksplit * T::kBlocks * 64;
+    if (!producer) {
+#pragma unroll
+      for (int o = 0; o < T::kOwn; ++o) part[((int64_t)s * T::kBlocks + ob[o]) * 64 + lane] = v[o];
+    }
+    if (!p.counters) return;  // no counters: sk_reduce_kernel adds the splits
+    wait_vmcnt<0>();  // the stores are in L2 before the counter moves
+    __syncthreads();
+    unsigned* flag = (unsigned*)(lds + T::kLds - 16);
+    if (threadIdx.x == 0) {
+      unsigned* ctr = p.counters + (t & 7) * kSkTilesPerXcd + (t >> 3);
+      const unsigned old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (old == (unsigned)p.ksplit - 1)  // every other split has arrived: clear for the next call
+        __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      *flag = old;
+    }
+    __syncthreads();
+    if (*flag != (unsigned)p.ksplit - 1 || producer) return;
+    // the partials of every split, added in split order (own sums in place of split s),
+    // loaded with sc0 (L1 bypassed, served by the XCD's L2)
+    const __amdgpu_buffer_rsrc_t pr =
+        __builtin_amdgcn_make_buffer_rsrc(part, (short)0, p.ksplit * T::kBlocks * 1024, 0x00020000);
+    // every load of a batch of eight splits goes out before the first add
+    floatx4 sum[T::kOwn] = {};
+    for (int s0 = 0; s0 < p.ksplit; s0 += 8) {
+      floatx4 pv[T::kOwn][8] = {};
+#pragma unroll
+      for (int o = 0; o < T::kOwn; ++o)
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          if (s0 + k < p.ksplit && s0 + k != s)
+            pv[o][k] = __builtin_bit_cast(
+                floatx4, __builtin_amdgcn_raw_buffer_load_b128(
+                             pr, (((s0 + k) * T::kBlocks + ob[o]) * 64 + lane) * 16, 0, 1));
+#pragma unroll
+      for (int o = 0; o < T::kOwn; ++o)
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          if (s0 + k < p.ksplit) sum[o] += s0 + k == s ? v[o] : pv[o][k];
+    }
+#pragma unroll
+    for (int o = 0; o < T::kOwn; ++o) v[o] = sum[o];
+  }
+  if (producer) return;
+#pragma unroll
+  for (int o = 0; o < T::kOwn; ++o) {
+    const int m = 16 * (ob[o] >> 2) + row;
+    if (m < p.M) store_half4(p, v[o], m, n0 + 16 * (ob[o] & 3) + 4 * grp);
+  }
+}
+
+// gemm_sk_kernel's split sums in a second launch, for streams without arrival counters: the
+// same additions in the same order as the last workgroup of a tile (from 0.f, split 0 first),
+// so both paths give the same bits.  One thread per (tile, 16 x 16 block, lane).
+template <int MT>
+__global__ __launch_bounds__(256) void sk_reduce_kernel(Params p) {
+  using T = SkTile<MT>;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)p.tiles * T::kBlocks * 64) return;
+  const int lane = (int)(idx & 63);
+  const int b = (int)((idx >> 6) % T::kBlocks);
+  const int t = (int)(idx / (64 * T::kBlocks));
+  const floatx4* part = (const floatx4*)p.partial + (int64_t)t * p.ksplit * T::kBlocks * 64;
+  floatx4 sum = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < p.ksplit; ++s) sum += part[((int64_t)s * T::kBlocks + b) * 64 + lane];
+  const int m = 16 * (b >> 2) + (lane & 15);
+  if (m < p.M) store_half4(p, sum, m, t * kNTile + 16 * (b & 3) + 4 * (lane >> 4));
+}
+
+// Arrival counters of gemm_sk_kernel: one per column tile and stream slot, laid out
+// [XCD group][tile / 8] so that each XCD group's counters share no cache line with another's.
+__device__ __attribute__((aligned(256))) unsigned sk_counters[kSkStreamSlots * kSkMaxTiles];
+
+// Whether the dispatcher puts block ids congruent modulo 8 on one XCD on this device: a probe
+// launch records every block's XCC_ID.
+__global__ __launch_bounds__(64) void xcd_probe_kernel(unsigned* out) {
+  if (threadIdx.x == 0) {
+    unsigned x;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+    out[blockIdx.x] = x & 0xf;
   }
 }
 
@@ -593,7 +752,6 @@ __global__ __launch_bounds__(64 * kW, kNorm ? 1 : 2) void gemv_kernel(Params p) 
   const bool m_ok = m < p.M;
   // MFMA output column j depends on X row j only, and the columns of rows past M are never
   // stored: those lanes read zeros (or, from the normalized rows in LDS, a valid row)
-  const int mc = m_ok ? m : p.M - 1;
   const int groups = p.K / kGroup;
   // fused norm: the workgroup's (at most 16, in practice a few) rows are normalized once
   // into LDS, [rows, K] fp16, and the X operand is read from there
@@ -806,19 +964,20 @@ struct Plan {
   int splits;
   int gemv_rows;
   bool library;  // prefill-sized: dequantize once, then a plain fp16 GEMM (rocBLAS)
+  bool sk;       // packed weights, 17..64 rows: gemm_sk_kernel (K split added in-launch)
 };
 
 // Dispatch thresholds (rows of X), chosen by measurement on MI355X: the one-pass kernel
 // up to 16 rows, the tiled split-K kernels up to 128, the library GEMM above.
 constexpr int kGemvMaxM = 16;
 constexpr int kLibraryMinM = 129;
-constexpr int kCus = 256;  // MI355X compute units
 
-// int4: packed weights, whose 64-row tiles run gemm_dma_kernel<64> at one workgroup per CU.
-inline Plan plan(int64_t M, int64_t N, int64_t K, bool int4) {
+// int4: packed weights.  cus: compute units of the device.
+inline Plan plan(int64_t M, int64_t N, int64_t K, bool int4, int cus) {
   Plan pl;
   pl.gemv_rows = 0;
   pl.library = false;
+  pl.sk = false;
   if (M >= kLibraryMinM) {
     pl.library = true;
     pl.mt = 0;
@@ -832,6 +991,17 @@ inline Plan plan(int64_t M, int64_t N, int64_t K, bool int4) {
     return pl;
   }
   const int64_t groups = K / kGroup;
+  const int64_t tiles = (N + kNTile - 1) / kNTile;
+  if (int4 && M <= 64) {
+    // one workgroup per (column tile, K split), at most eight groups each, about one per CU
+    pl.sk = true;
+    pl.mt = M <= 32 ? 32 : 64;
+    const int64_t lo = (groups + kSkMaxGroups - 1) / kSkMaxGroups;
+    const int64_t s = std::max<int64_t>(lo, std::min<int64_t>(groups, cus / tiles));
+    const int64_t per = (groups + s - 1) / s;
+    pl.splits = (int)((groups + per - 1) / per);
+    return pl;
+  }
   pl.mt = M <= 16 ? 16 : M <= 32 ? 32 : M <= 64 ? 64 : 128;
   const int64_t wgs = ((N + kNTile - 1) / kNTile) * ((M + pl.mt - 1) / pl.mt);
   int64_t s = 1;
@@ -840,10 +1010,6 @@ inline Plan plan(int64_t M, int64_t N, int64_t K, bool int4) {
     // keep the fp32 partials (written and read once) below the weight bytes
     const int64_t cap = std::max<int64_t>(1, K / (16 * std::max<int64_t>(M, 1)));
     s = std::min<int64_t>(std::min<int64_t>(s, cap), groups);
-    // One workgroup per CU fits the packed 64-row kernel: a second round of workgroups
-    // costs more than a finer K split saves (33..48 rows, QKV + O: 26-28 -> 22-23 us per
-    // layer).  The fp16-weight kernel holds two per CU and keeps the finer split.
-    if (int4 && pl.mt == 64) s = std::max<int64_t>(1, std::min<int64_t>(s, kCus / wgs));
   }
   // every split gets the same whole number of groups
   const int64_t per = (groups + s - 1) / std::max<int64_t>(s, 1);
@@ -903,11 +1069,86 @@ int check_linear(const char* fn, const void* x, int64_t x_stride, int64_t M, int
   return FI_OK;
 }
 
-// Packed weights at 17..64 rows go through gemm_dma_kernel when its scale table holds a
-// split's groups and its 32-bit copy offsets cover the operands.
-bool dma_ok(const fi::gemm::Params& p, const fi::gemm::Plan& pl) {
+// Arrival counters of gemm_sk_kernel for each device: kSkStreamSlots sets (one per stream
+// that runs split calls; other streams add their splits in a second launch), each zero at
+// load and left zero by every call.  They are used on a device only after xcd_probe_kernel
+// has shown that block ids congruent modulo 8 run on one XCD.
+constexpr int kSkMaxDevices = 64;
+struct SkDevice {
+  int state = 0;  // 0: not probed, 1: usable, -1: not usable
+  unsigned* counters = nullptr;
+  hipStream_t streams[fi::gemm::kSkStreamSlots] = {};
+  int used = 0;
+};
+
+std::mutex& sk_mutex() {
+  static std::mutex mu;
+  return mu;
+}
+
+SkDevice& sk_device(int dev) {
+  static SkDevice devs[kSkMaxDevices];
+  return devs[dev];
+}
+
+// One probe launch on `st` (the device's first split call): 2048 blocks record their XCC_ID.
+bool sk_probe(int dev, hipStream_t st) {
+  constexpr int kBlocks = 2048;
+  int cur = -1;
+  if (hipGetDevice(&cur) != hipSuccess) return false;
+  if (cur != dev && hipSetDevice(dev) != hipSuccess) return false;
+  hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+  (void)hipThreadExchangeStreamCaptureMode(&mode);
+  bool ok = false;
+  unsigned* d = nullptr;
+  std::vector<unsigned> h(kBlocks, 0u);
+  if (hipMalloc((void**)&d, kBlocks * sizeof(unsigned)) == hipSuccess) {
+    hipLaunchKernelGGL(fi::gemm::xcd_probe_kernel, dim3(kBlocks), dim3(64), 0, st, d);
+    ok = hipGetLastError() == hipSuccess &&
+         hipMemcpyAsync(h.data(), d, kBlocks * sizeof(unsigned), hipMemcpyDeviceToHost, st) ==
+             hipSuccess &&
+         hipStreamSynchronize(st) == hipSuccess;
+    for (int i = 8; ok && i < kBlocks; ++i) ok = h[i] == h[i & 7];
+    (void)hipFree(d);
+  }
+  (void)hipThreadExchangeStreamCaptureMode(&mode);
+  if (cur != dev) (void)hipSetDevice(cur);
+  return ok;
+}
+
+// The counter set of `st`, or nullptr when split calls on it take the two-launch path.
+unsigned* sk_counters_for(hipStream_t st) {
+  int dev = -1;
+  hipDevice_t d;
+  if (hipStreamGetDevice(st, &d) == hipSuccess) dev = (int)d;
+  if (dev < 0 || dev >= kSkMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(sk_mutex());
+  SkDevice& sd = sk_device(dev);
+  if (sd.state == 0) {
+    // the probe synchronizes: not while `st` is being captured or an error is pending
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone ||
+        hipPeekAtLastError() != hipSuccess)
+      return nullptr;
+    void* base = nullptr;
+    int cur = -1;
+    bool ok = hipGetDevice(&cur) == hipSuccess && (cur == dev || hipSetDevice(dev) == hipSuccess);
+    ok = ok && hipGetSymbolAddress(&base, HIP_SYMBOL(fi::gemm::sk_counters)) == hipSuccess;
+    if (cur >= 0 && cur != dev) (void)hipSetDevice(cur);
+    sd.counters = (unsigned*)base;
+    sd.state = ok && base && sk_probe(dev, st) ? 1 : -1;
+  }
+  if (sd.state != 1) return nullptr;
+  for (int i = 0; i < sd.used; ++i)
+    if (sd.streams[i] == st) return sd.counters + (size_t)i * fi::gemm::kSkMaxTiles;
+  if (sd.used == fi::gemm::kSkStreamSlots) return nullptr;
+  sd.streams[sd.used] = st;
+  return sd.counters + (size_t)(sd.used++) * fi::gemm::kSkMaxTiles;
+}
+
+// gemm_sk_kernel addresses X and the weight tile rows with 32-bit buffer offsets.
+bool dma_ok_sk(const fi::gemm::Params& p, const fi::gemm::Plan& pl) {
   using namespace fi::gemm;
-  if ((pl.mt != 32 && pl.mt != 64) || p.groups_per_split > kDmaMaxGroups) return false;
   const int64_t x_span = (int64_t)pl.mt * p.x_stride * 2 + (int64_t)p.K * 2;
   const int64_t w_span = (int64_t)kNTile * p.w_stride + p.K / 2;
   return x_span < (1ll << 31) - 4096 && w_span < (1ll << 31) - 4096;
@@ -919,6 +1160,33 @@ void launch_linear(const fi::gemm::Params& base, bool int4, const fi::gemm::Plan
                    void* workspace, hipStream_t st) {
   using namespace fi::gemm;
   Params p = base;
+  if (pl.sk && dma_ok_sk(p, pl)) {
+    // the split's arrival counters; without them (more than kSkMaxTiles column tiles, a
+    // stream past the per-device sets, a device whose dispatch does not group block ids by
+    // XCD, or a first call under graph capture) the workgroups only store their partials and
+    // sk_reduce_kernel adds them
+    const int groups = p.K / kGroup;
+    p.groups_per_split = (groups + pl.splits - 1) / pl.splits;
+    p.partial = (float*)workspace;
+    p.tiles = (p.N + kNTile - 1) / kNTile;
+    p.ksplit = pl.splits;
+    p.counters = pl.splits > 1 && p.tiles <= kSkMaxTiles ? sk_counters_for(st) : nullptr;
+    const dim3 grid((unsigned)(8 * pl.splits * ((p.tiles + 7) / 8)));
+    const dim3 block((kSkWaves + kSkLoaders) * 64);
+    if (pl.mt == 32)
+      hipLaunchKernelGGL(gemm_sk_kernel<32>, grid, block, 0, st, p);
+    else
+      hipLaunchKernelGGL(gemm_sk_kernel<64>, grid, block, 0, st, p);
+    if (pl.splits > 1 && !p.counters) {
+      const int64_t threads = (int64_t)p.tiles * 4 * (pl.mt / 16) * 64;
+      const dim3 rgrid((unsigned)((threads + 255) / 256));
+      if (pl.mt == 32)
+        hipLaunchKernelGGL(sk_reduce_kernel<32>, rgrid, dim3(256), 0, st, p);
+      else
+        hipLaunchKernelGGL(sk_reduce_kernel<64>, rgrid, dim3(256), 0, st, p);
+    }
+    return;
+  }
   if (kNorm || pl.gemv_rows) {
     p.partial = nullptr;
     p.groups_per_split = p.K / kGroup;
@@ -946,18 +1214,11 @@ void launch_linear(const fi::gemm::Params& base, bool int4, const fi::gemm::Plan
     else                                                                                    \
       hipLaunchKernelGGL((gemm_kernel<MT, false>), grid, dim3(kThreads), 0, st, p);          \
   } while (0)
-  if (int4 && dma_ok(p, pl)) {
-    if (pl.mt == 32)
-      hipLaunchKernelGGL(gemm_dma_kernel<32>, grid, dim3(kDmaThreads), 0, st, p);
-    else
-      hipLaunchKernelGGL(gemm_dma_kernel<64>, grid, dim3(kDmaThreads), 0, st, p);
-  } else {
-    switch (pl.mt) {
-      case 16: FI_GEMM_LAUNCH(16); break;
-      case 32: FI_GEMM_LAUNCH(32); break;
-      case 64: FI_GEMM_LAUNCH(64); break;
-      default: FI_GEMM_LAUNCH(128); break;
-    }
+  switch (pl.mt) {
+    case 16: FI_GEMM_LAUNCH(16); break;
+    case 32: FI_GEMM_LAUNCH(32); break;
+    case 64: FI_GEMM_LAUNCH(64); break;
+    default: FI_GEMM_LAUNCH(128); break;
   }
 #undef FI_GEMM_LAUNCH
   if (pl.splits > 1) {
@@ -992,11 +1253,19 @@ fi::gemm::Params make_params(const void* x, int64_t x_stride, int64_t M, int64_t
   p.groups_per_split = 0;
   p.norm_w = nullptr;
   p.eps = 0.f;
+  p.tiles = 0;
+  p.ksplit = 1;
+  p.counters = nullptr;
   return p;
 }
 
+// fp32 partials of a split call: gemm_sk_kernel's [tile][split][MT x 64] blocks, which also
+// hold the two-launch path's [split][M][N] for the same split
 size_t split_bytes(int64_t M, int64_t N, const fi::gemm::Plan& pl) {
-  return pl.splits > 1 ? (size_t)pl.splits * M * N * sizeof(float) : 0;
+  using fi::gemm::kNTile;
+  if (pl.splits <= 1) return 0;
+  if (pl.sk) return (size_t)pl.splits * ((N + kNTile - 1) / kNTile) * pl.mt * kNTile * sizeof(float);
+  return (size_t)pl.splits * M * N * sizeof(float);
 }
 
 // The norm is fused into the decode kernel for a few rows (each workgroup normalizes them
@@ -1031,8 +1300,9 @@ Layout layout(int64_t M, int64_t N, int64_t K, const fi::gemm::Plan& pl, bool in
 // What the size queries report: the larger of the packed and the fp16 weight forms.
 size_t workspace_bytes_for(int64_t M, int64_t N, int64_t K, bool norm) {
   using fi::gemm::plan;
-  return std::max(layout(M, N, K, plan(M, N, K, true), true, norm).total,
-                  layout(M, N, K, plan(M, N, K, false), false, norm).total);
+  const int cus = fi::device_cu_count(nullptr);
+  return std::max(layout(M, N, K, plan(M, N, K, true, cus), true, norm).total,
+                  layout(M, N, K, plan(M, N, K, false, cus), false, norm).total);
 }
 
 // One linear-layer call on any path; norm_w non-null applies RMSNorm to X first.
@@ -1044,7 +1314,7 @@ int run_linear(const char* fn, const void* x, int64_t x_stride, int64_t M, int64
   using namespace fi::gemm;
   const bool int4 = scales != nullptr;
   const bool norm = norm_w != nullptr;
-  const Plan pl = plan(M, N, K, int4);
+  const Plan pl = plan(M, N, K, int4, device_cu_count(st));
   const Layout l = layout(M, N, K, pl, int4, norm);
   if (l.total && (!workspace || workspace_bytes < l.total || ((uintptr_t)workspace & 255))) {
     set_error("%s: workspace of %zu bytes (256-byte aligned) needed, %zu given", fn, l.total,

@@ -10,7 +10,13 @@
 * int4_matmul with packed weights within the fp32-accumulation bound of the float64
   product on the dequantized weights, for decode-sized M (1..64, split-K) and prefill
   sizes, odd N, strided X; the speed mode (dequantized fp16 weights) within the same
-  bound.
+  bound;
+* the split-K kernel that adds its K splits in the same launch (17..64 rows, packed
+  weights): shapes whose tile and split counts change from call to call on one stream
+  (each call leaves its arrival counters at zero for the next), calls on two streams in
+  flight together (each stream has its own counters), and streams past the per-device
+  counter sets, which take the two-launch path: all within the same bound, and the same
+  bits on every stream that has counters.
 """
 
 import numpy as np
@@ -140,12 +146,10 @@ def test_int4_matmul_strided_x_and_batch_dims(hip):
     _check(out.reshape(14, N), x.reshape(14, K).numpy(), dequantize_int4(packed, scales).cpu().numpy())
 
 
-# 17..64 rows run the LDS-staged kernel (gemm_dma_kernel): one K group, a two-way K split
-# whose second part is shorter, an 11-way split of 64 groups, partial last column tiles,
-# strided X rows, a split capped to one workgroup per CU (48 rows of the QKV shape), an
-# N that is not a multiple of 4 with and without a K split (scalar partial and output
-# stores), and a grid of 257 column tiles with no K split (fp16 output written from the
-# staged tile)
+# 17..64 rows run the split-K kernel (gemm_sk_kernel): one K group, a two-way K split
+# whose second part is shorter, an 8-way split of 64 groups, partial last column tiles,
+# strided X rows, the QKV shape at 33 and 48 rows, an N that is not a multiple of 4 with
+# and without a K split (scalar output stores), and a grid of 257 column tiles
 @pytest.mark.parametrize("M,N,K,pad", [(17, 64, 128, 0), (20, 130, 640, 0), (40, 70, 8192, 264),
                                        (64, 200, 3072, 512), (33, 5120, 3072, 8),
                                        (48, 5120, 3072, 0), (36, 130, 3072, 0), (17, 66, 128, 0),
@@ -185,7 +189,7 @@ def test_int4_matmul_prefill_size_sampled(hip):
 
 
 def test_int4_matmul_workspace(hip):
-    """A split-K call (dequantized weights, 40 rows) with a caller workspace: the same
+    """Split-K calls (dequantized weights, 17..64 rows) with a caller workspace: the same
     bits as with the cached one, one workspace reused across shapes, and too small a
     workspace rejected before launch."""
     banner("int4_matmul workspace")
@@ -208,9 +212,10 @@ def test_int4_matmul_workspace(hip):
         a = int4_matmul(x[:m], w16, workspace=ws)
         b = int4_matmul(x[:m], w16)
         assert torch.equal(a, b)
+    # the size query covers both weight forms; the packed form needs all of it at 40 rows
     out = torch.empty(M, N, dtype=torch.float16, device=DEV)
-    rc = lib.fi_int4_matmul(x.data_ptr(), K, M, K, w16.data_ptr(), K, None, 0, N, 128,
-                            out.data_ptr(), N, ws.data_ptr(), need - 16,
+    rc = lib.fi_int4_matmul(x.data_ptr(), K, M, K, packed.data_ptr(), K // 2, scales.data_ptr(),
+                            K // 128, N, 128, out.data_ptr(), N, ws.data_ptr(), need - 16,
                             _lib.stream_handle(torch.device(DEV)))
     assert rc == _lib.FI_ERR_WORKSPACE
 
@@ -272,3 +277,75 @@ def test_other_group_sizes(hip, gs):
     xn = rms_norm(x.to(DEV), nw.to(DEV))
     torch.cuda.synchronize()
     _check(fused, xn.cpu().numpy(), w16)
+
+
+def _packed(seed, N, K):
+    from fast_infer_amd import quantize_int4_groupwise
+    w = _weights(seed, N, K, 0.02)
+    return quantize_int4_groupwise(torch.from_numpy(w).to(DEV))
+
+
+def test_int4_split_k_shapes_change_between_calls(hip):
+    """One stream, shapes whose column-tile and K-split counts differ from call to call,
+    three rounds: every call within the bound (a counter left non-zero by one call would
+    make a later call finish a tile before all its splits are stored)."""
+    banner("int4_matmul split-K: changing shapes on one stream")
+    from fast_infer_amd import dequantize_int4, int4_matmul
+
+    shapes = [(64, 5120, 3072), (17, 200, 640), (40, 1000, 1024), (64, 3072, 3072),
+              (33, 130, 8192), (64, 64, 128)]
+    ws = {shape: _packed(sum(shape), shape[1], shape[2]) for shape in shapes}
+    g = torch.Generator().manual_seed(5)
+    xs = {shape: torch.randn(shape[0], shape[2], generator=g).half() for shape in shapes}
+    for _ in range(3):
+        for shape in shapes:
+            packed, scales = ws[shape]
+            out = int4_matmul(xs[shape].to(DEV), (packed, scales))
+            torch.cuda.synchronize()
+            _check(out, xs[shape].numpy(), dequantize_int4(packed, scales).cpu().numpy())
+
+
+def test_int4_split_k_two_streams_in_flight(hip):
+    """Alternating calls on two streams with no synchronization between them: each stream
+    has its own arrival counters, so the calls may overlap; every output has the same bits
+    as a call on the default stream."""
+    banner("int4_matmul split-K: two streams in flight")
+    from fast_infer_amd import int4_matmul
+
+    N, K = 5120, 3072
+    packed, scales = _packed(21, N, K)
+    g = torch.Generator(device=DEV).manual_seed(22)
+    xs = [torch.randn(64, K, device=DEV, generator=g).half() for _ in range(8)]
+    refs = [int4_matmul(x, (packed, scales)) for x in xs]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(device=DEV), torch.cuda.Stream(device=DEV)]
+    outs = [None] * len(xs)
+    for rep in range(4):
+        for i, x in enumerate(xs):
+            with torch.cuda.stream(streams[i % 2]):
+                outs[i] = int4_matmul(x, (packed, scales))
+        torch.cuda.synchronize()
+        for i in range(len(xs)):
+            assert torch.equal(outs[i], refs[i]), (rep, i)
+
+
+def test_int4_split_k_streams_past_the_counter_sets(hip):
+    """More streams than the per-device counter sets (16): the streams without one take the
+    two-launch path (partials, then a reduction launch); all within the bound."""
+    banner("int4_matmul split-K: 20 streams")
+    from fast_infer_amd import dequantize_int4, int4_matmul
+
+    N, K = 3072, 3072
+    packed, scales = _packed(31, N, K)
+    w16 = dequantize_int4(packed, scales).cpu().numpy()
+    g = torch.Generator().manual_seed(32)
+    x = torch.randn(64, K, generator=g).half()
+    xd = x.to(DEV)
+    streams = [torch.cuda.Stream(device=DEV) for _ in range(20)]
+    outs = []
+    for st in streams:
+        with torch.cuda.stream(st):
+            outs.append(int4_matmul(xd, (packed, scales)))
+        st.synchronize()
+    for out in outs:
+        _check(out, x.numpy(), w16)
