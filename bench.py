@@ -10,7 +10,8 @@ the K/V pools rotated over four copies (2 GiB) so the 256 MB last-level cache ca
 serve them.  The same line carries:
 
 * ``prefill`` — causal prefill batch 4 x seq 4096 with the K/V pool write, TFLOP/s;
-* ``decode_b1_ctx256`` / ``prefill_b1_s512`` — the small configurations (latency);
+* ``decode_b1_ctx256`` / ``prefill_b1_s512`` — the small configurations (latency), per
+  eager call and per call of a HIP graph replay (GPU time without host launch cost);
 * ``decode_step_28layer_b64_paged`` — the same step with the device block manager (one
   append per step) and the fused RoPE + pool write per layer before attention;
 * ``int4_linear`` — the INT4 QKV / O projections around attention (decode batch 64 and 1
@@ -27,7 +28,10 @@ serve them.  The same line carries:
   host's cores on a bounded sample, plus the eager torch fp32 oracle.
 
 Timing uses HIP events on torch's current stream, which is the stream every
-fast_infer_amd kernel is launched on.  Inputs are resident in HBM before timing.
+fast_infer_amd kernel is launched on.  Inputs are resident in HBM before timing, and
+every section rotates the inputs it reads over copies that together exceed 320 MB
+(decode pools, prefill q/k/v, RoPE projections, the 28 layers' INT4 weights), so the
+256 MB last-level cache does not serve them from one call to the next.
 """
 
 from __future__ import annotations
@@ -117,6 +121,34 @@ class Timer:
         torch.cuda.synchronize()
         return start.elapsed_time(end) / 1e3 / steps  # seconds per call
 
+    def graph(self, fn, calls: int, steps: int, warmup: int) -> float:
+        """Seconds per call of fn with `calls` calls captured once into a HIP graph and the
+        graph replayed: the GPU time of the calls without the host's per-launch cost."""
+        torch = self.torch
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(calls):
+                fn()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(calls):
+                fn()
+        t = self.run(graph.replay, steps, warmup)
+        del graph
+        return t / calls
+
+
+# Inputs that a section reads on every call are kept in enough copies to exceed this many
+# bytes, and the calls rotate over them, so the 256 MB last-level cache cannot serve them.
+ROTATE_BYTES = 320 << 20
+
+
+def _copies(nbytes: int) -> int:
+    return max(2, -(-ROTATE_BYTES // max(1, nbytes)))
+
 
 def _table(torch, lens, pool_blocks, seed, width):
     perm = torch.randperm(pool_blocks, generator=torch.Generator().manual_seed(seed)).int()
@@ -156,26 +188,35 @@ def bench_decode_b32(torch, fi, timer, steps, warmup, dev):
     return dict(t=t, bytes=nbytes, gbs=gbs, lens=lens, q=q, pools=pools[0], table=table)
 
 
-def bench_prefill(torch, fi, timer, steps, warmup, dev, B, S, pool_blocks, seed, warm_s=0.0):
+def bench_prefill(torch, fi, timer, steps, warmup, dev, B, S, pool_blocks, seed, warm_s=0.0,
+                  graph=False):
     from fast_infer_amd import roofline as R
 
     g = torch.Generator(device=dev).manual_seed(seed)
-    q = torch.randn(B, S, HQ, D, device=dev, generator=g, dtype=torch.float16).transpose(1, 2)
-    k = torch.randn(B, S, HKV, D, device=dev, generator=g, dtype=torch.float16).transpose(1, 2)
-    v = torch.randn(B, S, HKV, D, device=dev, generator=g, dtype=torch.float16).transpose(1, 2)
+    copies = _copies(B * S * (HQ + 2 * HKV) * D * 2)
+    qkv = []
+    for _ in range(copies):
+        qkv.append(tuple(
+            torch.randn(B, S, H, D, device=dev, generator=g, dtype=torch.float16).transpose(1, 2)
+            for H in (HQ, HKV, HKV)))
     kc = torch.zeros(pool_blocks, BS, HKV, D, device=dev, dtype=torch.float16)
     vc = torch.zeros_like(kc)
     per_row = pool_blocks // B
     table = torch.randperm(pool_blocks, generator=torch.Generator().manual_seed(seed)).int()
     table = table.view(B, per_row).to(dev)
+    it = [0]
 
     def step():
+        q, k, v = qkv[it[0] % copies]
+        it[0] += 1
         fi.flash_attention(q, k, v, k_cache=kc, v_cache=vc, block_table=table)
 
     t = timer.run(step, steps, warmup, warm_s)
+    t_graph = timer.graph(step, copies, steps, warmup) if graph else None
     flops = R.prefill_flops(B, HQ, S, D)
-    return dict(t=t, flops=flops, tflops=flops / t / 1e12, q=q, k=k, v=v,
-                scatter_bytes=R.prefill_scatter_bytes(B, S, HKV, D))
+    q, k, v = qkv[0]
+    return dict(t=t, t_graph=t_graph, flops=flops, tflops=flops / t / 1e12, q=q, k=k, v=v,
+                copies=copies, scatter_bytes=R.prefill_scatter_bytes(B, S, HKV, D))
 
 
 def bench_decode_b1(torch, fi, timer, steps, warmup, dev):
@@ -196,8 +237,9 @@ def bench_decode_b1(torch, fi, timer, steps, warmup, dev):
         fi.paged_attention(q, kc, vc, table, BS, 256)
 
     t = timer.run(step, steps, warmup)
+    t_graph = timer.graph(step, copies, steps, warmup)
     nbytes = R.decode_bytes([256], HQ, HKV, D, BS)
-    return dict(t=t, bytes=nbytes, gbs=nbytes / t / 1e9)
+    return dict(t=t, t_graph=t_graph, bytes=nbytes, gbs=nbytes / t / 1e9)
 
 
 def bench_decode_28layer(torch, fi, timer, steps, warmup, dev):
@@ -233,9 +275,12 @@ def bench_rope(torch, fi, timer, steps, warmup, dev, B, T, start, pool_blocks, r
     from fast_infer_amd import roofline as R
 
     g = torch.Generator(device=dev).manual_seed(7)
-    qkv = torch.randn(B, T, (HQ + 2 * HKV) * D, device=dev, generator=g, dtype=torch.float16)
-    q, k, v = qkv.split([HQ * D, HKV * D, HKV * D], dim=-1)
-    q, k, v = q.view(B, T, HQ, D), k.view(B, T, HKV, D), v.view(B, T, HKV, D)
+    copies = _copies(B * T * (HQ + 2 * HKV) * D * 2)
+    views = []
+    for _ in range(copies):
+        qkv = torch.randn(B, T, (HQ + 2 * HKV) * D, device=dev, generator=g, dtype=torch.float16)
+        q, k, v = qkv.split([HQ * D, HKV * D, HKV * D], dim=-1)
+        views.append((q.view(B, T, HQ, D), k.view(B, T, HKV, D), v.view(B, T, HKV, D)))
     cos, sin = fi.precompute_freqs(D, 4096, device=dev)
     cos, sin = cos.half(), sin.half()
     kc = torch.zeros(pool_blocks, BS, HKV, D, device=dev, dtype=torch.float16)
@@ -244,8 +289,11 @@ def bench_rope(torch, fi, timer, steps, warmup, dev, B, T, start, pool_blocks, r
     table = torch.randperm(pool_blocks, generator=torch.Generator().manual_seed(7)).int()
     table = table.view(B, per_row).to(dev)
     q_out = torch.empty(B, T, HQ, D, device=dev, dtype=torch.float16)
+    it = [0]
 
     def step():
+        q, k, v = views[it[0] % copies]
+        it[0] += 1
         fi.rope_store_kv(q, k, v, cos, sin, start, kc, vc, table, return_k=return_k,
                          q_out=q_out)
 
@@ -563,13 +611,20 @@ def main():
         }
     if "small" in only:
         d1 = bench_decode_b1(torch, fi, timer, steps, warm, dev)
-        p1 = bench_prefill(torch, fi, timer, steps, warm, dev, 1, 512, 64, 1, warm_s=WARM_S)
+        p1 = bench_prefill(torch, fi, timer, steps, warm, dev, 1, 512, 64, 1, warm_s=WARM_S,
+                           graph=True)
         out["decode_b1_ctx256"] = {"us_per_call": round(d1["t"] * 1e6, 2),
-                                   "GB/s": round(d1["gbs"], 1), "bytes": d1["bytes"]}
+                                   "graph_us_per_call": round(d1["t_graph"] * 1e6, 2),
+                                   "GB/s": round(d1["gbs"], 1),
+                                   "graph_GB/s": round(d1["bytes"] / d1["t_graph"] / 1e9, 1),
+                                   "bytes": d1["bytes"]}
         out["prefill_b1_s512"] = {"us_per_call": round(p1["t"] * 1e6, 2),
-                                  "TFLOP/s": round(p1["tflops"], 2)}
-        print(f"[bench] small: decode b1 {d1['t'] * 1e6:.1f} us, prefill s512 "
-              f"{p1['t'] * 1e6:.1f} us", file=sys.stderr, flush=True)
+                                  "graph_us_per_call": round(p1["t_graph"] * 1e6, 2),
+                                  "TFLOP/s": round(p1["tflops"], 2),
+                                  "graph_TFLOP/s": round(p1["flops"] / p1["t_graph"] / 1e12, 2)}
+        print(f"[bench] small: decode b1 {d1['t'] * 1e6:.1f} us (graph "
+              f"{d1['t_graph'] * 1e6:.1f}), prefill s512 {p1['t'] * 1e6:.1f} us (graph "
+              f"{p1['t_graph'] * 1e6:.1f})", file=sys.stderr, flush=True)
     if "e2e" in only:
         e = bench_decode_28layer(torch, fi, timer, steps, warm, dev)
         out["decode_28layer_b64"] = {

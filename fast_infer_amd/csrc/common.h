@@ -34,6 +34,16 @@ void clear_error();
 int check_launch(const char* what);
 // Compute units of the device that runs `stream` (cached per device).
 int device_cu_count(hipStream_t stream);
+// Whether workgroups whose block ids are congruent modulo 8 run on one XCD on the device of
+// `st` (one probe launch and a synchronous copy on `st` at the device's first call; false,
+// and not yet probed, while `st` is being captured).
+bool xcd_groups_ok(hipStream_t st);
+// Slot (0 .. slots - 1) of `st` among the streams that asked for `purpose` on its device, in
+// order of first request, or -1 once `slots` streams hold one.  Kernels keep one set of
+// cross-workgroup counters per slot, so calls on different streams never share counters.
+constexpr int kXcdPurposes = 1;  // the split-K INT4 GEMM
+constexpr int kXcdMaxSlots = 16;
+int xcd_stream_slot(hipStream_t st, int purpose, int slots);
 
 // ---------------------------------------------------------------------------
 // Device helpers

@@ -20,9 +20,9 @@
 #include <stdlib.h>
 
 #include <algorithm>
-#include <type_traits>
+#include <atomic>
 #include <mutex>
-#include <vector>
+#include <type_traits>
 
 #include "common.h"
 
@@ -357,7 +357,7 @@ constexpr int kSkLoaders = 4;                       // loading waves
 constexpr int kSkMaxGroups = 8;                     // K groups per workgroup
 constexpr int kSkTilesPerXcd = 256;                 // counters per XCD group and stream
 constexpr int kSkMaxTiles = 8 * kSkTilesPerXcd;     // column tiles per call
-constexpr int kSkStreamSlots = 16;                  // streams per device with their own counters
+constexpr int kSkStreamSlots = kXcdMaxSlots;        // streams per device with their own counters
 
 template <int MT>
 struct SkTile {
@@ -674,15 +674,6 @@ __global__ __launch_bounds__(256) void sk_reduce_kernel(Params p) {
 // [XCD group][tile / 8] so that each XCD group's counters share no cache line with another's.
 __device__ __attribute__((aligned(256))) unsigned sk_counters[kSkStreamSlots * kSkMaxTiles];
 
-// Whether the dispatcher puts block ids congruent modulo 8 on one XCD on this device: a probe
-// launch records every block's XCC_ID.
-__global__ __launch_bounds__(64) void xcd_probe_kernel(unsigned* out) {
-  if (threadIdx.x == 0) {
-    unsigned x;
-    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
-    out[blockIdx.x] = x & 0xf;
-  }
-}
 
 // Prefill-sized calls: the MFMA kernels above spend most of their time dequantizing (each
 // weight is dequantized once per row tile) at these sizes, so the weight is dequantized once
@@ -1069,81 +1060,31 @@ int check_linear(const char* fn, const void* x, int64_t x_stride, int64_t M, int
   return FI_OK;
 }
 
-// Arrival counters of gemm_sk_kernel for each device: kSkStreamSlots sets (one per stream
-// that runs split calls; other streams add their splits in a second launch), each zero at
-// load and left zero by every call.  They are used on a device only after xcd_probe_kernel
-// has shown that block ids congruent modulo 8 run on one XCD.
-constexpr int kSkMaxDevices = 64;
-struct SkDevice {
-  int state = 0;  // 0: not probed, 1: usable, -1: not usable
-  unsigned* counters = nullptr;
-  hipStream_t streams[fi::gemm::kSkStreamSlots] = {};
-  int used = 0;
-};
-
-std::mutex& sk_mutex() {
-  static std::mutex mu;
-  return mu;
-}
-
-SkDevice& sk_device(int dev) {
-  static SkDevice devs[kSkMaxDevices];
-  return devs[dev];
-}
-
-// One probe launch on `st` (the device's first split call): 2048 blocks record their XCC_ID.
-bool sk_probe(int dev, hipStream_t st) {
-  constexpr int kBlocks = 2048;
-  int cur = -1;
-  if (hipGetDevice(&cur) != hipSuccess) return false;
-  if (cur != dev && hipSetDevice(dev) != hipSuccess) return false;
-  hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
-  (void)hipThreadExchangeStreamCaptureMode(&mode);
-  bool ok = false;
-  unsigned* d = nullptr;
-  std::vector<unsigned> h(kBlocks, 0u);
-  if (hipMalloc((void**)&d, kBlocks * sizeof(unsigned)) == hipSuccess) {
-    hipLaunchKernelGGL(fi::gemm::xcd_probe_kernel, dim3(kBlocks), dim3(64), 0, st, d);
-    ok = hipGetLastError() == hipSuccess &&
-         hipMemcpyAsync(h.data(), d, kBlocks * sizeof(unsigned), hipMemcpyDeviceToHost, st) ==
-             hipSuccess &&
-         hipStreamSynchronize(st) == hipSuccess;
-    for (int i = 8; ok && i < kBlocks; ++i) ok = h[i] == h[i & 7];
-    (void)hipFree(d);
-  }
-  (void)hipThreadExchangeStreamCaptureMode(&mode);
-  if (cur != dev) (void)hipSetDevice(cur);
-  return ok;
-}
-
-// The counter set of `st`, or nullptr when split calls on it take the two-launch path.
+// Arrival counters of gemm_sk_kernel for the stream `st`: one set per stream slot (other
+// streams add their splits in a second launch), each zero at load and left zero by every
+// call; only on a device where block ids congruent modulo 8 share an XCD.
 unsigned* sk_counters_for(hipStream_t st) {
-  int dev = -1;
+  using fi::gemm::kSkMaxTiles;
+  constexpr int kMaxDevices = 64;
+  static std::atomic<unsigned*> base[kMaxDevices];
+  if (!fi::xcd_groups_ok(st)) return nullptr;
+  const int slot = fi::xcd_stream_slot(st, 0, fi::gemm::kSkStreamSlots);
+  if (slot < 0) return nullptr;
   hipDevice_t d;
-  if (hipStreamGetDevice(st, &d) == hipSuccess) dev = (int)d;
-  if (dev < 0 || dev >= kSkMaxDevices) return nullptr;
-  std::lock_guard<std::mutex> lock(sk_mutex());
-  SkDevice& sd = sk_device(dev);
-  if (sd.state == 0) {
-    // the probe synchronizes: not while `st` is being captured or an error is pending
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone ||
-        hipPeekAtLastError() != hipSuccess)
-      return nullptr;
-    void* base = nullptr;
+  if (hipStreamGetDevice(st, &d) != hipSuccess || (int)d < 0 || (int)d >= kMaxDevices) return nullptr;
+  unsigned* b = base[(int)d].load();
+  if (!b) {
     int cur = -1;
-    bool ok = hipGetDevice(&cur) == hipSuccess && (cur == dev || hipSetDevice(dev) == hipSuccess);
-    ok = ok && hipGetSymbolAddress(&base, HIP_SYMBOL(fi::gemm::sk_counters)) == hipSuccess;
-    if (cur >= 0 && cur != dev) (void)hipSetDevice(cur);
-    sd.counters = (unsigned*)base;
-    sd.state = ok && base && sk_probe(dev, st) ? 1 : -1;
+    if (hipGetDevice(&cur) != hipSuccess) return nullptr;
+    if (cur != (int)d && hipSetDevice((int)d) != hipSuccess) return nullptr;
+    void* addr = nullptr;
+    const bool ok = hipGetSymbolAddress(&addr, HIP_SYMBOL(fi::gemm::sk_counters)) == hipSuccess;
+    if (cur != (int)d) (void)hipSetDevice(cur);
+    if (!ok || !addr) return nullptr;
+    b = (unsigned*)addr;
+    base[(int)d].store(b);
   }
-  if (sd.state != 1) return nullptr;
-  for (int i = 0; i < sd.used; ++i)
-    if (sd.streams[i] == st) return sd.counters + (size_t)i * fi::gemm::kSkMaxTiles;
-  if (sd.used == fi::gemm::kSkStreamSlots) return nullptr;
-  sd.streams[sd.used] = st;
-  return sd.counters + (size_t)(sd.used++) * fi::gemm::kSkMaxTiles;
+  return b + (size_t)slot * kSkMaxTiles;
 }
 
 // gemm_sk_kernel addresses X and the weight tile rows with 32-bit buffer offsets.
