@@ -788,13 +788,42 @@ __global__ __launch_bounds__(64 * kW, kNorm ? 1 : 2) void gemv_kernel(Params p) 
   // the first chunk's weights are in flight while the rows are normalized; the scheduling
   // barriers keep every load of a chunk ahead of its math (the scheduler would otherwise
   // start the math after the first few loads and issue the rest one latency later)
-  load_chunk(wave);
-  __builtin_amdgcn_sched_barrier(0);
   if constexpr (kNorm) {
-    for (int r = wave; r < rows_n; r += kW)
+    // Wave r normalizes row r.  Its x row and the norm weight are loaded before the first
+    // chunk's weights: loads complete in issue order, so the norm waits for its own data
+    // only and runs while the weights stream in.  Rows longer than kRowChunks * 512, and rows
+    // past the kW-th, are normalized after the weights' loads by norm_row_to.
+    const bool in_regs = p.K <= kRowChunks * 512 && wave < rows_n;  // uniform
+    u32x4 xr_v[kRowChunks], nw_v[kRowChunks];
+    if (in_regs) {
+      const half_t* xrow = p.x + (int64_t)(blockIdx.y * 16 + wave) * p.x_stride;
+#pragma unroll
+      for (int i = 0; i < kRowChunks; ++i) {
+        const int k = lane * 8 + i * 512;
+        xr_v[i] = k < p.K ? *(const u32x4*)(xrow + k) : u32x4{0, 0, 0, 0};
+        nw_v[i] = k < p.K ? *(const u32x4*)(p.norm_w + k) : u32x4{0, 0, 0, 0};
+      }
+    }
+    load_chunk(wave);
+    __builtin_amdgcn_sched_barrier(0);
+    if (in_regs) {
+      float sq = 0.f;
+#pragma unroll
+      for (int i = 0; i < kRowChunks; ++i) sq += sum_sq8(xr_v[i]);
+      const float r = rsqrtf(wave_sum(sq) / (float)p.K + p.eps);
+#pragma unroll
+      for (int i = 0; i < kRowChunks; ++i) {
+        const int k = lane * 8 + i * 512;
+        if (k < p.K) *(u32x4*)(xn + wave * p.K + k) = norm8(xr_v[i], r, nw_v[i]);
+      }
+    }
+    for (int r = in_regs ? wave + kW : wave; r < rows_n; r += kW)
       norm_row_to(p.x + (int64_t)(blockIdx.y * 16 + r) * p.x_stride, p.norm_w, p.K, p.eps,
                   xn + r * p.K, lane);
     __syncthreads();
+  } else {
+    load_chunk(wave);
+    __builtin_amdgcn_sched_barrier(0);
   }
 
   // two accumulators, alternating by k-step, halve the chain of dependent MFMAs
