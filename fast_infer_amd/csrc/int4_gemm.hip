@@ -7,8 +7,16 @@
 // The weight the reference multiplies with is fp16(q * scale) (matmul.py:83-84 and
 // :309-326): one rounding of an exact product, which is what v_pk_mul_f16 computes.
 //
-// GEMM: C[m, n] = fp16( sum_k X[m, k] * W[n, k] ), fp32 accumulation (matmul.py:14-132,
-// :135-186).  One workgroup = 4 waves = 64 output columns (16 per wave) x MT rows, over a
+// C[m, n] = fp16( sum_k X[m, k] * W[n, k] ), fp32 accumulation (matmul.py:14-132,
+// :135-186), by the rows M of X:
+//   M <= 16          gemv_kernel: one workgroup per 16 output columns, K split over its waves;
+//   17..64, packed   gemm_sk_kernel: loader and multiplier waves, K split over workgroups
+//                    whose partial sums are added inside the launch (sk_reduce_kernel when
+//                    the stream has no counters);
+//   17..128          gemm_kernel (packed weights from 65 rows), below;
+//   >= 129           the weight dequantized once into the workspace, then a library fp16 GEMM.
+//
+// gemm_kernel: one workgroup = 4 waves = 64 output columns (16 per wave) x MT rows, over a
 // slice of the K groups.  Per 128-wide group, X[MT, 128] is staged in LDS (double
 // buffered, rows padded to 272 bytes so the 16 rows a wave reads are on distinct banks);
 // each lane loads 16 bytes of its weight row (32 int4 values), dequantizes them in
