@@ -372,7 +372,7 @@ struct SkTile {
   static constexpr int kX = MT * 256;              // X tile of one group
   static constexpr int kW = kNTile * 64;           // W tile of one group
   static constexpr int kSlot = kX + kW;
-  static constexpr int kXCopies = MT / 4;          // 1 KiB copies of 4 X rows
+  static constexpr int kXCopies = MT / 4;          // 1 KiB copies (16 rows of one X panel)
   static constexpr int kCopies = kXCopies + 4;     // + 4 of 16 W columns
   static constexpr int kMSub = MT / 16;            // 16-row blocks
   static constexpr int kBlocks = 4 * kMSub;        // 16 x 16 output blocks
@@ -458,18 +458,22 @@ __global__ __launch_bounds__((kSkWaves + kSkLoaders) * 64, 1) void gemm_sk_kerne
     const rsrc_t xr = raw_rsrc(p.x, (int)((min(MT, p.M) - 1) * p.x_stride * 2 + p.K * 2));
     const rsrc_t wr = raw_rsrc(p.w + (int64_t)n0 * p.w_stride,
                               (int)((min(kNTile, p.N - n0) - 1) * p.w_stride + p.K / 2));
-    // copy cc of a group: X rows 4cc .. 4cc + 3 (row 4cc + lane / 16, slot lane % 16 <- chunk
-    // slot ^ (row % 16)), then W columns 16cw .. 16cw + 15 (column 16cw + lane / 4, slot
-    // lane % 4 <- 16-byte chunk slot ^ ((column / 2) % 4), so that the weight reads of eight
-    // consecutive columns fall on distinct banks).  Loading wave l issues X copies cc = l,
-    // l + 4, ... and W copy cw = l of every group; per-lane offsets at group 0.
+    // X of a group is stored as four panels, panel c holding 16-byte chunks 4c .. 4c + 3 of
+    // every row (64 bytes per row); sub-chunk kk of row r of panel c sits at slot
+    // kk ^ ((r / 2) % 4) ^ c.  Loading wave l fills panel l: its copy i covers rows 16i ..
+    // 16i + 15 (row 16i + lane / 4, slot lane % 4).  Then W columns 16cw .. 16cw + 15 (column
+    // 16cw + lane / 4, slot lane % 4 <- 16-byte chunk slot ^ ((column / 2) % 4)); loading wave
+    // l issues W copy cw = l of every group.  Both layouts make the fragment reads of 16
+    // consecutive rows (columns) at one chunk conflict-free; per-lane offsets at group 0.
     constexpr int kXPer = T::kXCopies / kSkLoaders;
-    static_assert(T::kXCopies % kSkLoaders == 0, "X copies split evenly over the loading waves");
+    static_assert(T::kXCopies % kSkLoaders == 0 && kSkLoaders == 4,
+                  "one X panel per loading wave, whole 16-row copies");
     int xoff[kXPer];
 #pragma unroll
     for (int i = 0; i < kXPer; ++i) {
-      const int r = 4 * (l + kSkLoaders * i) + (lane >> 4);
-      xoff[i] = r * (int)p.x_stride * 2 + (((lane & 15) ^ (r & 15)) << 4);
+      const int r = 16 * i + (lane >> 2);
+      const int kk = (lane & 3) ^ ((lane >> 3) & 3) ^ l;
+      xoff[i] = r * (int)p.x_stride * 2 + ((4 * l + kk) << 4);
     }
     const int woff = (16 * l + (lane >> 2)) * (int)p.w_stride + (((lane & 3) ^ ((lane >> 3) & 3)) << 4);
     auto issue = [&](int u0, int gp) {
@@ -479,7 +483,7 @@ __global__ __launch_bounds__((kSkWaves + kSkLoaders) * 64, 1) void gemm_sk_kerne
         const int g = g_begin + u;
 #pragma unroll
         for (int i = 0; i < kXPer; ++i)
-          lds_copy16(xr, base + (l + kSkLoaders * i) * 1024, xoff[i], g * 256);
+          lds_copy16(xr, base + l * (MT * 64) + i * 1024, xoff[i], g * 256);
         lds_copy16(wr, base + T::kX + l * 1024, woff, g * (kGroup / 2));
       }
     };
@@ -536,7 +540,8 @@ __global__ __launch_bounds__((kSkWaves + kSkLoaders) * 64, 1) void gemm_sk_kerne
         const char* slot = lds + u * T::kSlot;
 #pragma unroll
         for (int ii = 0; ii < kMSub; ++ii)
-          xv[b][ii] = *(const u32x4*)(slot + (16 * ii + row) * 256 + (((4 * grp + k) ^ row) << 4));
+          xv[b][ii] = *(const u32x4*)(slot + grp * (MT * 64) + (16 * ii + row) * 64 +
+                                      ((k ^ ((row >> 1) & 3) ^ grp) << 4));
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj)
           wd[b][jj] = *(const uint32_t*)(slot + T::kX + (16 * (2 * h + jj) + row) * 64 +
