@@ -41,8 +41,8 @@ FILE_FLAGS = {
 }
 
 
-# rocBLAS runs the plain fp16 GEMM of prefill-sized linear layers (int4_gemm.hip).
-LINK_LIBS = ["-lrocblas"]
+# Extra libraries linked into the extension (none: every kernel is built here).
+LINK_LIBS: list = []
 
 
 def _hipcc() -> str:

@@ -14,7 +14,8 @@
 //                    whose partial sums are added inside the launch (sk_reduce_kernel when
 //                    the stream has no counters);
 //   17..128          gemm_kernel (packed weights from 65 rows), below;
-//   >= 129           the weight dequantized once into the workspace, then a library fp16 GEMM.
+//   >= 129           the weight dequantized once into the workspace, then
+//                    ping_pong_gemm_kernel, an fp16 GEMM.
 //
 // gemm_kernel: one workgroup = 4 waves = 64 output columns (16 per wave) x MT rows, over a
 // slice of the K groups.  Per 128-wide group, X[MT, 128] is staged in LDS (double
@@ -24,7 +25,6 @@
 // operand.  In k-step s (0..3) of a group, lane group g = lane/16 supplies k = 32g + 8s
 // .. +7: the 16 bytes one lane loads are exactly its four k-steps.  Small grids split the
 // K groups over blockIdx.z; a second kernel adds the fp32 partials in a fixed order.
-#include <rocblas/rocblas.h>
 #include <stdlib.h>
 
 #include <algorithm>
@@ -690,51 +690,224 @@ __device__ __attribute__((aligned(256))) unsigned sk_counters[kSkStreamSlots * k
 
 // Prefill-sized calls: the MFMA kernels above spend most of their time dequantizing (each
 // weight is dequantized once per row tile) at these sizes, so the weight is dequantized once
-// into the workspace and the plain fp16 GEMM runs in rocBLAS (fp16 in and out, fp32
-// accumulation).  One rocBLAS handle per device, created on first use; the stream is set
-// per call under a lock.
-struct BlasState {
-  std::mutex mu;
-  rocblas_handle handle[64] = {};
+// into the workspace and a plain fp16 GEMM runs on it: ping_pong_gemm_kernel.
+//
+// C[M, N] = X[M, K] * W[N, K]^T, fp16 in and out, fp32 accumulation, K a multiple of 64.
+// One workgroup per 256 x 256 tile of C, eight waves, two per SIMD: waves w and w + 4 share
+// SIMD w % 4 (checked on gfx950 with a probe reading HW_REG_HW_ID).  Wave w owns 64 rows
+// (m, 64 * (w / 2)..) x 128 columns (n, 128 * (w % 2)..) of the tile: 8 x 4 MFMA tiles of
+// v_mfma_f32_16x16x32_f16, W as the A operand and X^T as the B operand, 128 fp32 sums.
+// Per 64-wide K step the tile's X and W rows (128 bytes each, 16-byte chunk c of row r at
+// slot c ^ ((r / 2) % 8), so the 16 rows a quarter-wave reads fall on distinct banks) are
+// copied global->LDS with buffer_load ... lds into one of two 64 KiB stages.
+// The two halves of the workgroup (waves 0-3, waves 4-7) take turns, one barrier-separated
+// phase apart: while one half runs its step's 64 MFMAs on fragments held in registers, the
+// other reads the next step's 24 fragments from LDS and issues copies.  Each SIMD then
+// always has one wave feeding its matrix core and one loading, without either waiting for
+// the other's LDS latency.  Copies of step t + 1 go out two phases after the last read of
+// their stage and are waited for (vmcnt) by the wave that issued them before the phase in
+// which step t + 1 is first read.
+constexpr int kPpTile = 256;             // rows and columns of C per workgroup
+constexpr int kPpK = 64;                 // K per step
+constexpr int kPpThreads = 512;
+constexpr int kPpRowB = kPpK * 2;        // bytes per LDS row
+constexpr int kPpOperand = kPpTile * kPpRowB;  // 32 KiB: X or W rows of one step
+constexpr int kPpStage = 2 * kPpOperand;       // 64 KiB: X rows, then W rows
+
+struct PpParams {
+  const half_t* x;
+  int64_t ldx;
+  const half_t* w;
+  int64_t ldw;
+  half_t* o;
+  int64_t ldo;
+  int M, N, K;
+  int tiles_m;
+  int band;     // tiles_m / 8 when tiles_m % 8 == 0 (row tiles banded by XCD), else 0
+  int vec_out;  // output rows 16-byte aligned and N % 8 == 0: 16-byte stores
 };
 
-inline BlasState& blas_state() {
-  static BlasState s;
-  return s;
+// A workgroup barrier that nothing crosses: the compiler's scheduler may not move
+// instructions (MFMAs included) over it, nor memory accesses (the copies are inline asm it
+// does not track).
+__device__ __forceinline__ void pp_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
 }
 
-// C[M, N] (ldc) = X[M, K] (ldx) * W[N, K]^T (ldw), all fp16 row-major, fp32 accumulation.
-inline int blas_gemm(const half_t* x, int64_t ldx, const half_t* w, int64_t ldw, half_t* out,
-                     int64_t ldc, int M, int N, int K, hipStream_t st) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
-    set_error("fi_int4_matmul: no current HIP device");
-    return FI_ERR_HIP;
+__global__ __launch_bounds__(kPpThreads, 1) void ping_pong_gemm_kernel(PpParams p) {
+  __shared__ __attribute__((aligned(16))) char lds[2 * kPpStage];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int half = wave >> 2;               // 0: waves 0-3, 1: waves 4-7 (one phase behind)
+  const int wn = wave & 1, wm = wave >> 1;  // wave tile: columns 128 * wn.., rows 64 * wm..
+  // Tile order: with p.band, block id L runs on XCD L % 8 and XCD e takes row tiles
+  // e * band .. e * band + band - 1 against every column tile, so the X rows of its tiles
+  // stay in its own L2; otherwise row tiles vary fastest.
+  int tm, tn;
+  {
+    const int L = blockIdx.x;
+    if (p.band) {
+      const int t = L >> 3;
+      tm = (L & 7) * p.band + t % p.band;
+      tn = t / p.band;
+    } else {
+      tm = L % p.tiles_m;
+      tn = L / p.tiles_m;
+    }
   }
-  BlasState& bs = blas_state();
-  std::lock_guard<std::mutex> lock(bs.mu);
-  if (!bs.handle[dev] && rocblas_create_handle(&bs.handle[dev]) != rocblas_status_success) {
-    bs.handle[dev] = nullptr;
-    set_error("fi_int4_matmul: rocblas_create_handle failed");
-    return FI_ERR_HIP;
+  const int m0 = tm * kPpTile, n0 = tn * kPpTile;
+  const int rows_x = min(kPpTile, p.M - m0), rows_w = min(kPpTile, p.N - n0);
+  // descriptors over exactly the tile's rows: lanes of rows past M or N read zeros
+  const rsrc_t xr = raw_rsrc(p.x + (int64_t)m0 * p.ldx,
+                             (int)(((int64_t)(rows_x - 1) * p.ldx + p.K) * 2));
+  const rsrc_t wr = raw_rsrc(p.w + (int64_t)n0 * p.ldw,
+                             (int)(((int64_t)(rows_w - 1) * p.ldw + p.K) * 2));
+  // this wave copies rows 32w .. 32w + 31 of X and of W: four instructions of 8 rows each
+  // per operand; lane l fills slot l % 8 of row r0 + l / 8 with chunk (l % 8) ^ ((r / 2) % 8)
+  int xoff[4], woff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 32 * wave + 8 * i + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    xoff[i] = r < rows_x ? (int)((int64_t)r * p.ldx * 2) + (c << 4) : 0x7ffffff0;
+    woff[i] = r < rows_w ? (int)((int64_t)r * p.ldw * 2) + (c << 4) : 0x7ffffff0;
   }
-  rocblas_handle h = bs.handle[dev];
-  if (rocblas_set_stream(h, st) != rocblas_status_success) {
-    set_error("fi_int4_matmul: rocblas_set_stream failed");
-    return FI_ERR_HIP;
+  const uint32_t lds0 = lds_addr(lds);
+  const int steps = p.K / kPpK;
+  auto issue = [&](int kt) {
+    const uint32_t base = lds0 + (kt & 1) * kPpStage;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      lds_copy16(xr, base + (32 * wave + 8 * i) * kPpRowB, xoff[i], kt * kPpRowB);
+      lds_copy16(wr, base + kPpOperand + (32 * wave + 8 * i) * kPpRowB, woff[i], kt * kPpRowB);
+    }
+  };
+
+  floatx4 acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  // fragment (k-substep s, tile i): row 16i + fr, chunk 4s + fg; rows 16i + fr share
+  // (row / 2) % 8 with row fr
+  const int fr = lane & 15, fg = lane >> 4;
+  const int sw = (fr >> 1) & 7;
+  const int xrow0 = (64 * wm + fr) * kPpRowB, wrow0 = kPpOperand + (128 * wn + fr) * kPpRowB;
+  half8 wf[2][8], xf[2][4];
+
+  issue(0);
+  if (steps > 1) issue(1);
+  if (steps > 1)
+    wait_vmcnt<8>();  // step 0 (loads complete in issue order)
+  else
+    wait_vmcnt<0>();
+  pp_barrier();
+  if (half) pp_barrier();  // waves 4-7 start one phase later
+  for (int kt = 0; kt < steps; ++kt) {
+    // LOAD phase: this step's fragments.  Waves 0-3 also copy step kt + 1 into the stage
+    // of step kt - 1, which waves 4-7 finished reading in the previous phase.
+    {
+      const char* st = lds + (kt & 1) * kPpStage;
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          wf[s][i] = as_half8(
+              *(const u32x4*)(st + wrow0 + i * 16 * kPpRowB + (((4 * s + fg) ^ sw) << 4)));
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          xf[s][j] = as_half8(
+              *(const u32x4*)(st + xrow0 + j * 16 * kPpRowB + (((4 * s + fg) ^ sw) << 4)));
+      }
+      if (half == 0 && kt >= 1 && kt + 1 < steps) issue(kt + 1);
+      wait_lgkmcnt0();  // the stage may be refilled once this phase ends
+      if (half == 1) wait_vmcnt<0>();  // this wave's copies of step kt + 1
+    }
+    pp_barrier();
+    // COMPUTE phase: 64 MFMAs on registers.  Waves 4-7 copy step kt + 2 into the stage of
+    // step kt, which both halves have now read.
+    {
+      if (half == 1 && kt + 2 < steps) issue(kt + 2);
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[i][j] = mfma16x16x32(wf[s][i], xf[s][j], acc[i][j]);
+      if (half == 0) wait_vmcnt<0>();  // this wave's copies of step kt + 1
+    }
+    pp_barrier();
   }
-  const float alpha = 1.f, beta = 0.f;
-  // column-major view: C^T [N, M] = op(W^T)^T ... = W [N, K] x X^T [K, M]
-  const rocblas_status rs = rocblas_gemm_ex(
-      h, rocblas_operation_transpose, rocblas_operation_none, N, M, K, &alpha, w,
-      rocblas_datatype_f16_r, (rocblas_int)ldw, x, rocblas_datatype_f16_r, (rocblas_int)ldx, &beta,
-      out, rocblas_datatype_f16_r, (rocblas_int)ldc, out, rocblas_datatype_f16_r,
-      (rocblas_int)ldc, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
-  if (rs != rocblas_status_success) {
-    set_error("fi_int4_matmul: rocblas_gemm_ex failed (%d)", (int)rs);
-    return FI_ERR_HIP;
+  if (!half) pp_barrier();  // every wave passes the same number of barriers
+
+  // Lane (m = 16j + fr, fg) holds C[m][16i + 4fg .. +3] of the wave's block.  Rows go
+  // through the wave's own 16 KiB of LDS (fp16, 256 bytes a row, chunk c of row m at
+  // c ^ (m % 16)) so that 16 lanes store one row's 256 bytes.
+  char* cs = lds + wave * (64 * 256);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int m = 16 * j + fr;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = 2 * i + (fg >> 1);
+      *(half4*)(cs + m * 256 + ((c ^ (m & 15)) << 4) + ((fg & 1) << 3)) = to_half4(acc[i][j]);
+    }
   }
-  return FI_OK;
+  wave_lds_sync();
+  const int sr = lane >> 4, sc = lane & 15;
+  const int gn = n0 + 128 * wn + 8 * sc;
+#pragma unroll 4
+  for (int q = 0; q < 16; ++q) {
+    const int m = 4 * q + sr;
+    const u32x4 v = *(const u32x4*)(cs + m * 256 + ((sc ^ (m & 15)) << 4));
+    const int gm = m0 + 64 * wm + m;
+    if (gm >= p.M || gn >= p.N) continue;
+    half_t* dst = p.o + (int64_t)gm * p.ldo + gn;
+    if (p.vec_out) {
+      *(u32x4*)dst = v;
+    } else {
+      const half8 h = as_half8(v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (gn + e < p.N) dst[e] = h[e];
+    }
+  }
+}
+
+// C[M, N] (ldc) = X[M, K] (ldx) * W[N, K]^T (ldw), all fp16 row-major, fp32 accumulation;
+// K a multiple of 64, rows of X and W 16-byte aligned.
+inline int f16_gemm(const half_t* x, int64_t ldx, const half_t* w, int64_t ldw, half_t* out,
+                    int64_t ldc, int64_t M, int64_t N, int64_t K, hipStream_t st) {
+  if (K % kPpK || ((int64_t)(kPpTile - 1) * std::max(ldx, ldw) + K) * 2 >= 0x7ffffff0) {
+    set_error("fi_int4_matmul: 256 rows of X or W span 2^31 bytes or more");
+    return FI_ERR_UNSUPPORTED;
+  }
+  PpParams p;
+  p.x = x;
+  p.ldx = ldx;
+  p.w = w;
+  p.ldw = ldw;
+  p.o = out;
+  p.ldo = ldc;
+  p.M = (int)M;
+  p.N = (int)N;
+  p.K = (int)K;
+  p.tiles_m = (int)((M + kPpTile - 1) / kPpTile);
+  const int64_t tiles_n = (N + kPpTile - 1) / kPpTile;
+  const int64_t tiles = p.tiles_m * tiles_n;
+  if (tiles > 0x7fffffff) {
+    set_error("fi_int4_matmul: too many output tiles");
+    return FI_ERR_UNSUPPORTED;
+  }
+  p.band = p.tiles_m % 8 == 0 ? p.tiles_m / 8 : 0;
+  p.vec_out = ((uintptr_t)out & 15) == 0 && ldc % 8 == 0 && N % 8 == 0;
+  hipLaunchKernelGGL(ping_pong_gemm_kernel, dim3((unsigned)tiles), dim3(kPpThreads), 0, st, p);
+  return check_launch("fi_int4_matmul");
 }
 
 // Decode-sized calls (16 rows of X per blockIdx.y): one workgroup per 16 output columns.
@@ -996,23 +1169,23 @@ struct Plan {
   int mt;
   int splits;
   int gemv_rows;
-  bool library;  // prefill-sized: dequantize once, then a plain fp16 GEMM (rocBLAS)
+  bool dense;  // prefill-sized: dequantize once, then a plain fp16 GEMM (f16_gemm)
   bool sk;       // packed weights, 17..64 rows: gemm_sk_kernel (K split added in-launch)
 };
 
 // Dispatch thresholds (rows of X), chosen by measurement on MI355X: the one-pass kernel
-// up to 16 rows, the tiled split-K kernels up to 128, the library GEMM above.
+// up to 16 rows, the tiled split-K kernels up to 128, the plain fp16 GEMM above.
 constexpr int kGemvMaxM = 16;
-constexpr int kLibraryMinM = 129;
+constexpr int kDenseMinM = 129;
 
 // int4: packed weights.  cus: compute units of the device.
 inline Plan plan(int64_t M, int64_t N, int64_t K, bool int4, int cus) {
   Plan pl;
   pl.gemv_rows = 0;
-  pl.library = false;
+  pl.dense = false;
   pl.sk = false;
-  if (M >= kLibraryMinM) {
-    pl.library = true;
+  if (M >= kDenseMinM) {
+    pl.dense = true;
     pl.mt = 0;
     pl.splits = 1;
     return pl;
@@ -1057,7 +1230,7 @@ inline Plan plan(int64_t M, int64_t N, int64_t K, bool int4, int cus) {
 namespace {
 
 using fi::half_t;
-using fi::gemm::blas_gemm;
+using fi::gemm::f16_gemm;
 using fi::gemm::dequantize_kernel;
 using fi::gemm::rmsnorm_kernel;
 
@@ -1266,7 +1439,7 @@ size_t round256(int64_t n) { return (size_t)((n + 255) / 256 * 256); }
 size_t norm_rows_bytes(int64_t M, int64_t K) { return round256(M * K * 2); }
 
 // Workspace layout of a call: [normalized rows (separate norm pass)] [dequantized weight
-// (library path, packed weights)] [fp32 partials (split K)], each 256-byte aligned.
+// (dense path, packed weights)] [fp32 partials (split K)], each 256-byte aligned.
 struct Layout {
   size_t rows, weight, split, total;
 };
@@ -1274,7 +1447,7 @@ struct Layout {
 Layout layout(int64_t M, int64_t N, int64_t K, const fi::gemm::Plan& pl, bool int4, bool norm) {
   Layout l;
   l.rows = norm && !fuse_norm(M, K, pl) ? norm_rows_bytes(M, K) : 0;
-  l.weight = pl.library && int4 ? round256(N * K * 2) : 0;
+  l.weight = pl.dense && int4 ? round256(N * K * 2) : 0;
   l.split = round256((int64_t)split_bytes(M, N, pl));
   l.total = l.rows + l.weight + l.split;
   return l;
@@ -1304,7 +1477,7 @@ int run_linear(const char* fn, const void* x, int64_t x_stride, int64_t M, int64
               workspace ? workspace_bytes : (size_t)0);
     return FI_ERR_WORKSPACE;
   }
-  if (!pl.library && (M + (pl.mt ? pl.mt : 16) - 1) / (pl.mt ? pl.mt : 16) > 65535) {
+  if (!pl.dense && (M + (pl.mt ? pl.mt : 16) - 1) / (pl.mt ? pl.mt : 16) > 65535) {
     set_error("%s: M %lld too large", fn, (long long)M);
     return FI_ERR_UNSUPPORTED;
   }
@@ -1333,7 +1506,7 @@ int run_linear(const char* fn, const void* x, int64_t x_stride, int64_t M, int64
     p.x = normed;
     p.x_stride = K;
   }
-  if (pl.library) {
+  if (pl.dense) {
     const half_t* w16 = (const half_t*)w;
     int64_t ldw = w_stride;
     if (int4) {  // dequantize once into the workspace
@@ -1348,8 +1521,7 @@ int run_linear(const char* fn, const void* x, int64_t x_stride, int64_t M, int64
     }
     const int rc = check_launch(fn);
     if (rc != FI_OK) return rc;
-    return blas_gemm(p.x, p.x_stride, w16, ldw, (half_t*)out, out_stride, (int)M, (int)N,
-                     (int)K, st);
+    return f16_gemm(p.x, p.x_stride, w16, ldw, (half_t*)out, out_stride, M, N, K, st);
   }
   launch_linear<false>(p, int4, pl, ws + l.rows + l.weight, st);
   return check_launch(fn);

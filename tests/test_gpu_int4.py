@@ -188,6 +188,51 @@ def test_int4_matmul_prefill_size_sampled(hip):
     _check(out16[rows.to(DEV)], x[rows.to(DEV)].cpu().numpy(), w16.cpu().numpy())
 
 
+# 129 rows and up: the weight dequantized once, then the 256 x 256-tile fp16 GEMM
+# (ping_pong_gemm_kernel).  Shapes: partial row and column tiles, two K steps (K 128), row
+# tiles in multiples of 8 (the XCD-banded tile order) and not, N not a multiple of 8
+# (element stores), output rows with a stride and an output that is only 2-byte aligned
+# (element stores), X rows with a stride; packed and fp16 weights, every row against float64.
+@pytest.mark.parametrize("M,N,K,xpad,opad,ooff", [(129, 264, 128, 0, 0, 0),
+                                                  (257, 130, 1024, 8, 6, 1),
+                                                  (520, 640, 3072, 0, 0, 0),
+                                                  (300, 1288, 3072, 264, 8, 0),
+                                                  (2048, 256, 256, 0, 0, 0),
+                                                  (4096, 520, 512, 0, 16, 0),
+                                                  (2100, 72, 384, 0, 0, 3)])
+def test_int4_matmul_dense_path_shapes(hip, M, N, K, xpad, opad, ooff):
+    banner(f"int4_matmul dense M={M} N={N} K={K} x pad {xpad} out pad {opad} out offset {ooff}")
+    from fast_infer_amd import _lib, dequantize_int4, quantize_int4_groupwise
+
+    lib = _lib.load()
+    w = _weights(M + 3 * N, N, K, 0.02)
+    packed, scales = quantize_int4_groupwise(torch.from_numpy(w).to(DEV))
+    w16 = dequantize_int4(packed, scales)
+    g = torch.Generator(device=DEV).manual_seed(M + K)
+    xbig = torch.randn(M, K + xpad, device=DEV, generator=g).half()
+    x = xbig[:, 8:8 + K] if xpad else xbig
+    ld = N + opad
+    ws = torch.empty(lib.fi_int4_matmul_workspace_size(M, N, K), dtype=torch.uint8, device=DEV)
+    st = _lib.stream_handle(torch.device(DEV))
+    for form in ("packed", "fp16"):
+        buf = torch.full((M * ld + 8,), float("nan"), dtype=torch.float16, device=DEV)
+        out_ptr = buf.data_ptr() + 2 * ooff
+        if form == "packed":
+            rc = lib.fi_int4_matmul(x.data_ptr(), x.stride(0), M, K, packed.data_ptr(), K // 2,
+                                    scales.data_ptr(), K // 128, N, 128, out_ptr, ld,
+                                    ws.data_ptr(), ws.numel(), st)
+        else:
+            rc = lib.fi_int4_matmul(x.data_ptr(), x.stride(0), M, K, w16.data_ptr(), K, None, 0,
+                                    N, 128, out_ptr, ld, ws.data_ptr(), ws.numel(), st)
+        _lib.check(rc, "fi_int4_matmul")
+        torch.cuda.synchronize()
+        rows = buf[ooff:ooff + M * ld].view(M, ld)
+        _check(rows[:, :N], x.cpu().numpy(), w16.cpu().numpy())
+        # nothing written between rows or past the last one
+        assert torch.isnan(rows[:, N:]).all() and torch.isnan(buf[:ooff]).all()
+        assert torch.isnan(buf[ooff + M * ld:]).all()
+
+
 def test_int4_matmul_workspace(hip):
     """Split-K calls (dequantized weights, 17..64 rows) with a caller workspace: the same
     bits as with the cached one, one workspace reused across shapes, and too small a
