@@ -36,10 +36,11 @@
  *     [0, num_blocks) are never dereferenced: rows that map there are skipped.
  *   - `stream` is a hipStream_t (NULL = the legacy default stream).  Every call
  *     is asynchronous: it enqueues work and returns; nothing synchronises.
- *   - Calls are reentrant.  The library's only host-side state is the per-thread
- *     error message and, for prefill-sized fi_int4_matmul calls (M >= 129), one
- *     rocBLAS handle per device, created on first use under a mutex and kept until
- *     the process ends.
+ *   - Calls are reentrant.  The library's host-side state is the per-thread error
+ *     message and, per device, cached on first use: the CU count (an atomic), and,
+ *     under a mutex, the result of the workgroup-placement probe and the streams that
+ *     were given split-K counter sets (fi_int4_matmul, at most 16 per device).  No
+ *     other library is called.
  *   - Return value: FI_OK or an FI_ERR_* code; fi_last_error() then gives a
  *     message for the calling thread.
  *   - fp16 data.  head_dim: a multiple of 8 up to 128 for the attention entry points
@@ -305,6 +306,9 @@ FI_API int fi_kv_reset(int32_t* block_table, int64_t bt_stride, int64_t max_bloc
  *   fi_int4_dequantize and pass the fp16 weight.  Some shapes split K: then a workspace of
  *   fi_int4_matmul_workspace_size(M, N, K) bytes (enough for either weight form) is
  *   required (FI_ERR_WORKSPACE otherwise); calls that overlap in time must not share one.
+ *   From 129 rows packed weights are dequantized into that workspace and both forms run
+ *   a 256 x 256-tile fp16 GEMM kernel, which needs 256 rows of X (and of an fp16 W) to
+ *   span less than 2 GiB (FI_ERR_UNSUPPORTED otherwise).
  */
 FI_API size_t fi_int4_matmul_workspace_size(int64_t M, int64_t N, int64_t K);
 FI_API int fi_int4_matmul(const void* x, int64_t x_stride, int64_t M, int64_t K,
