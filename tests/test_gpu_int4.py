@@ -189,17 +189,19 @@ def test_int4_matmul_prefill_size_sampled(hip):
 
 
 # 129 rows and up: the weight dequantized once, then the 256 x 256-tile fp16 GEMM
-# (ping_pong_gemm_kernel).  Shapes: partial row and column tiles, two K steps (K 128), row
-# tiles in multiples of 8 (the XCD-banded tile order) and not, N not a multiple of 8
-# (element stores), output rows with a stride and an output that is only 2-byte aligned
-# (element stores), X rows with a stride; packed and fp16 weights, every row against float64.
+# (ping_pong_gemm_kernel).  Shapes: partial row and column tiles, two K steps (K 128) and
+# 128 (K 8192), row tiles in multiples of 8 (the XCD-banded tile order, also with a partial
+# last row tile) and not, N not a multiple of 8 (element stores), output rows with a stride
+# and an output that is only 2-byte aligned (element stores), X rows with a stride; packed
+# and fp16 weights, every row against float64.
 @pytest.mark.parametrize("M,N,K,xpad,opad,ooff", [(129, 264, 128, 0, 0, 0),
                                                   (257, 130, 1024, 8, 6, 1),
                                                   (520, 640, 3072, 0, 0, 0),
                                                   (300, 1288, 3072, 264, 8, 0),
                                                   (2048, 256, 256, 0, 0, 0),
                                                   (4096, 520, 512, 0, 16, 0),
-                                                  (2100, 72, 384, 0, 0, 3)])
+                                                  (2100, 72, 384, 0, 0, 3),
+                                                  (1800, 264, 8192, 0, 0, 0)])
 def test_int4_matmul_dense_path_shapes(hip, M, N, K, xpad, opad, ooff):
     banner(f"int4_matmul dense M={M} N={N} K={K} x pad {xpad} out pad {opad} out offset {ooff}")
     from fast_infer_amd import _lib, dequantize_int4, quantize_int4_groupwise
