@@ -193,3 +193,27 @@ def stream_handle(device: torch.device) -> int:
         index = device.index if device.index is not None else torch.cuda.current_device()
         return _raw_stream(index)
     return torch.cuda.current_stream(device).cuda_stream
+
+
+def tensor_stream(t: torch.Tensor) -> int:
+    """hipStream_t of torch's current stream on the device of the HIP tensor `t` (its
+    device index read as an int: no torch.device object is built)."""
+    if _raw_stream is not None:
+        return _raw_stream(t.get_device())
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+# Workspace sizes depend only on the integer sizes of a call: each distinct query is made
+# once.  The wrappers make them on every call, so this saves a foreign call per launch.
+_size_cache: dict[tuple, int] = {}
+
+
+def workspace_size(name: str, *sizes: int) -> int:
+    key = (name, sizes)
+    n = _size_cache.get(key)
+    if n is None:
+        n = getattr(load(), name)(*sizes)
+        if len(_size_cache) > 4096:
+            _size_cache.clear()
+        _size_cache[key] = n
+    return n

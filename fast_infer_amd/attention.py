@@ -28,31 +28,46 @@ def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
-def _rows_ok(t: torch.Tensor) -> bool:
+# The wrappers below run once per kernel launch; on the decode path their host time is of
+# the order of the GPU time, so they read each tensor's strides and pointer once, compare
+# dtypes by identity and devices by index (no torch.device objects).
+
+def _strides_ok(st: tuple, ptr: int) -> bool:
     """Innermost dim contiguous, other strides multiples of 8, 16-byte aligned base."""
-    if t.stride(-1) != 1:
+    if st[-1] != 1 or ptr % 16:
         return False
-    if any(s % 8 for s in t.stride()[:-1]):
-        return False
-    return t.data_ptr() % 16 == 0
+    for x in st[:-1]:
+        if x % 8:
+            return False
+    return True
 
 
-def _prep_rows(t: torch.Tensor) -> torch.Tensor:
-    return t if _rows_ok(t) else t.contiguous()
+def _rows_ok(t: torch.Tensor) -> bool:
+    return _strides_ok(t.stride(), t.data_ptr())
+
+
+def _prep_rows(t: torch.Tensor) -> tuple[torch.Tensor, tuple, int]:
+    """(t or a contiguous copy, its strides, its pointer) with rows the kernels can read."""
+    st, ptr = t.stride(), t.data_ptr()
+    if not _strides_ok(st, ptr):
+        t = t.contiguous()
+        st, ptr = t.stride(), t.data_ptr()
+    return t, st, ptr
 
 
 def _check_fp16_cuda(name: str, t: torch.Tensor) -> None:
-    if t.dtype != torch.float16:
+    if t.dtype is not torch.float16:
         raise TypeError(f"{name} must be float16, got {t.dtype}")
-    if t.device.type != "cuda":
+    if not t.is_cuda:
         raise RuntimeError(f"{name} must be on a HIP device (got {t.device}); "
                            "fast_infer_amd has no CPU path")
 
 
-def _check_table(block_table: torch.Tensor, device: torch.device) -> torch.Tensor:
-    if block_table.dtype != torch.int32:
+def _check_table(block_table: torch.Tensor, dev: int) -> torch.Tensor:
+    """block_table validated against the device index `dev` of q."""
+    if block_table.dtype is not torch.int32:
         raise TypeError(f"block_table must be int32, got {block_table.dtype}")
-    if block_table.device != device:
+    if block_table.get_device() != dev:
         raise RuntimeError("block_table must be on the same device as q")
     if block_table.dim() != 2:
         raise ValueError("block_table must be [batch, max_blocks_per_seq]")
@@ -91,10 +106,13 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     if num_kv_heads == 0 or num_heads % num_kv_heads:
         raise ValueError(f"num_heads {num_heads} is not a multiple of kv heads {num_kv_heads}")
     o = torch.empty_like(q)  # q's strides (:99)
-    q, k, v = _prep_rows(q), _prep_rows(k), _prep_rows(v)
+    q, qs, q_ptr = _prep_rows(q)
+    k, ks, k_ptr = _prep_rows(k)
+    v, vs, v_ptr = _prep_rows(v)
     # the kernel writes 16-byte rows; an output whose strides do not allow that is
     # computed into a contiguous buffer and copied into o at the end
     work = o if _rows_ok(o) else torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    ws_ = work.stride()
 
     kc = vc = bt = None
     n_pool = bt_stride = max_blocks = 0
@@ -108,7 +126,7 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
             raise ValueError(f"pool shape {tuple(k_cache.shape)} != {expect}")
         if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
             raise ValueError("pools must be contiguous")
-        bt = _check_table(block_table, q.device)
+        bt = _check_table(block_table, q.get_device())
         if bt.shape[0] < batch:
             raise ValueError("block_table has fewer rows than the batch")
         kc, vc = k_cache, v_cache
@@ -118,15 +136,13 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         return o
     lib = _lib.load()
     rc = lib.fi_flash_attention_fwd(
-        q.data_ptr(), k.data_ptr(), v.data_ptr(), work.data_ptr(),
+        q_ptr, k_ptr, v_ptr, work.data_ptr(),
         batch, num_heads, num_kv_heads, seq_len, head_dim,
-        q.stride(0), q.stride(1), q.stride(2),
-        k.stride(0), k.stride(1), k.stride(2),
-        v.stride(0), v.stride(1), v.stride(2),
-        work.stride(0), work.stride(1), work.stride(2),
+        qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2],
+        ws_[0], ws_[1], ws_[2],
         float(sm_scale),
         _ptr(kc), _ptr(vc), n_pool, block_size, _ptr(bt), bt_stride, max_blocks,
-        _lib.stream_handle(q.device))
+        _lib.tensor_stream(q))
     _lib.check(rc, "flash_attention")
     if work is not o:
         o.copy_(work)
@@ -168,54 +184,63 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
     num_tokens = int(num_tokens)
     if context_lens is None and num_tokens == 0:
         return torch.zeros_like(q)
-    if sm_scale is None:
-        sm_scale = q.shape[-1] ** -0.5
-
     batch, num_q_heads, head_dim = q.shape
+    if sm_scale is None:
+        sm_scale = head_dim ** -0.5
+
     _check_fp16_cuda("q", q)
     _check_fp16_cuda("k_cache", k_cache)
     _check_fp16_cuda("v_cache", v_cache)
-    if k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
+    pool_shape = k_cache.shape
+    if len(pool_shape) != 4 or v_cache.shape != pool_shape:
         raise ValueError("k_cache/v_cache must be [num_blocks, block_size, kv_heads, dim]")
-    num_kv_heads = k_cache.shape[2]
-    if k_cache.shape[1] != block_size or k_cache.shape[3] != head_dim:
-        raise ValueError(f"pool shape {tuple(k_cache.shape)} does not match block_size "
+    num_blocks, pool_bs, num_kv_heads, pool_dim = pool_shape
+    if pool_bs != block_size or pool_dim != head_dim:
+        raise ValueError(f"pool shape {tuple(pool_shape)} does not match block_size "
                          f"{block_size} / head_dim {head_dim}")
     if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
         raise ValueError("pools must be contiguous")
     if num_q_heads % num_kv_heads:
         raise ValueError(f"num_q_heads {num_q_heads} not a multiple of kv heads {num_kv_heads}")
-    block_table = _check_table(block_table, q.device)
-    if block_table.shape[0] < batch:
+    dev = q.get_device()
+    block_table = _check_table(block_table, dev)
+    bt_rows, bt_cols = block_table.shape
+    if bt_rows < batch:
         raise ValueError("block_table has fewer rows than the batch")
     if context_lens is not None:
-        if context_lens.dtype != torch.int32 or context_lens.device != q.device:
+        if context_lens.dtype is not torch.int32 or context_lens.get_device() != dev:
             context_lens = context_lens.to(device=q.device, dtype=torch.int32)
         if context_lens.numel() < batch:
             raise ValueError("context_lens has fewer entries than the batch")
-        context_lens = context_lens.contiguous()
+        if not context_lens.is_contiguous():
+            context_lens = context_lens.contiguous()
     o = torch.empty_like(q)  # q's strides (:216)
-    q = _prep_rows(q)
-    work = o if _rows_ok(o) else torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    q, qs, q_ptr = _prep_rows(q)
+    os_, o_ptr = o.stride(), o.data_ptr()
+    if _strides_ok(os_, o_ptr):
+        work = o
+    else:
+        work = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        os_, o_ptr = work.stride(), work.data_ptr()
     if batch == 0:
         return o
 
     lib = _lib.load()
-    need = lib.fi_paged_attention_workspace_size(batch, num_q_heads, num_kv_heads,
-                                                 max(num_tokens, 1), head_dim)
+    need = _lib.workspace_size("fi_paged_attention_workspace_size", batch, num_q_heads,
+                               num_kv_heads, max(num_tokens, 1), head_dim)
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
     ws_ptr = workspace.data_ptr() if (need and workspace is not None) else None
     ws_bytes = workspace.numel() * workspace.element_size() if ws_ptr else 0
     rc = lib.fi_paged_attention_fwd(
-        q.data_ptr(), q.stride(0), q.stride(1),
-        k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[0], block_size, num_kv_heads,
-        block_table.data_ptr(), block_table.stride(0), block_table.shape[1],
+        q_ptr, qs[0], qs[1],
+        k_cache.data_ptr(), v_cache.data_ptr(), num_blocks, block_size, num_kv_heads,
+        block_table.data_ptr(), block_table.stride(0), bt_cols,
         _ptr(context_lens), num_tokens,
-        work.data_ptr(), work.stride(0), work.stride(1),
+        o_ptr, os_[0], os_[1],
         batch, num_q_heads, head_dim, float(sm_scale),
         ws_ptr, ws_bytes,
-        _lib.stream_handle(q.device))
+        _lib.tensor_stream(q))
     _lib.check(rc, "paged_attention")
     if work is not o:
         o.copy_(work)

@@ -20,19 +20,32 @@ from . import _lib
 PACKED_GROUP = 128  # the group size the packed-weight kernels read (the reference's)
 
 
+# These wrappers run once per projection and decode step, where their host time is of the
+# order of the kernels': each tensor's shape, strides and pointer are read once, dtypes
+# compared by identity, devices checked with is_cuda, and workspace sizes cached.
+
 def _need_cuda(name: str, t: torch.Tensor) -> None:
-    if t.device.type != "cuda":
+    if not t.is_cuda:
         raise RuntimeError(f"{name} must be on a HIP device; fast_infer_amd has no CPU path")
 
 
-def _rows16(t: torch.Tensor, elem: int) -> torch.Tensor:
-    """t with unit inner stride, 16-byte aligned rows and row stride a multiple of 16 B."""
-    if (t.stride(-1) != 1 or t.data_ptr() % 16 or (t.stride(0) * elem) % 16
-            or t.stride(0) < t.shape[1]):
+def _rows16(t: torch.Tensor, elem: int) -> tuple[torch.Tensor, int, int]:
+    """(t with unit inner stride, 16-byte aligned rows and row stride a multiple of 16 B,
+    its row stride, its pointer) for a 2-D t."""
+    (s0, s1), ptr = t.stride(), t.data_ptr()
+    if s1 != 1 or ptr % 16 or (s0 * elem) % 16 or s0 < t.shape[1]:
         t = t.contiguous()
-        if t.data_ptr() % 16 or (t.stride(0) * elem) % 16:
+        s0, ptr = t.stride(0), t.data_ptr()
+        if ptr % 16 or (s0 * elem) % 16:
             raise ValueError("rows must be 16-byte aligned (K a multiple of 8 elements)")
-    return t
+    return t, s0, ptr
+
+
+def _norm_weight(w: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+    """An RMSNorm weight as a contiguous fp16 tensor on x's device."""
+    if w.dtype is not torch.float16 or w.get_device() != x.get_device():
+        w = w.to(device=x.device, dtype=torch.float16)
+    return w if w.is_contiguous() else w.contiguous()
 
 
 # Split-K calls need a workspace for their fp32 partials; one per (device, stream), grown
@@ -67,31 +80,29 @@ def int4_matmul(x: torch.Tensor, w, scales=None, groupsize: int = 128, *,
     fp16 values) and take the fp16 form."""
     _need_cuda("x", x)
     w = _other_group_size(w, groupsize)
-    N, K, wt, w_stride, s_ptr, s_stride, _keep = _weight_args(w, groupsize)
-    if x.shape[-1] != K:
-        raise ValueError(f"x has K = {x.shape[-1]}, the weight K = {K}")
+    N, K, w_ptr, w_stride, s_ptr, s_stride, _keep = _weight_args(w, groupsize)
+    x_shape = x.shape
+    if x_shape[-1] != K:
+        raise ValueError(f"x has K = {x_shape[-1]}, the weight K = {K}")
     if K % groupsize:
         raise ValueError(f"K ({K}) must be multiple of groupsize ({groupsize})")
-    if x.dtype != torch.float16:
+    if x.dtype is not torch.float16:
         x = x.to(torch.float16)
-    lead = x.shape[:-1]
-    x2 = _rows16(x.reshape(-1, K), 2)
+    x2, x_stride, x_ptr = _rows16(x if len(x_shape) == 2 else x.reshape(-1, K), 2)
     M = x2.shape[0]
     out = torch.empty(M, N, dtype=torch.float16, device=x.device)
     if M == 0 or N == 0:
-        return out.reshape(*lead, N)
-    lib = _lib.load()
-    stream = _lib.stream_handle(x.device)
-    need = lib.fi_int4_matmul_workspace_size(M, N, K)
+        return out if len(x_shape) == 2 else out.reshape(*x_shape[:-1], N)
+    stream = _lib.tensor_stream(x)
+    need = _lib.workspace_size("fi_int4_matmul_workspace_size", M, N, K)
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = _workspace(x.device, stream, need)
     ws_ptr = workspace.data_ptr() if need else None
     ws_bytes = workspace.numel() * workspace.element_size() if need else 0
-    rc = lib.fi_int4_matmul(x2.data_ptr(), x2.stride(0), M, K, wt.data_ptr(), w_stride, s_ptr,
-                            s_stride, N, groupsize, out.data_ptr(), out.stride(0), ws_ptr,
-                            ws_bytes, stream)
+    rc = _lib.load().fi_int4_matmul(x_ptr, x_stride, M, K, w_ptr, w_stride, s_ptr, s_stride, N,
+                                    groupsize, out.data_ptr(), N, ws_ptr, ws_bytes, stream)
     _lib.check(rc, "int4_matmul")
-    return out.reshape(*lead, N)
+    return out if len(x_shape) == 2 else out.reshape(*x_shape[:-1], N)
 
 
 _warned_group_sizes: set[int] = set()
@@ -117,28 +128,33 @@ def _other_group_size(w, groupsize: int):
 
 
 def _weight_args(w, groupsize: int):
-    """(N, K, weight tensor, its row stride, scales pointer, scales row stride, scales
-    tensor kept alive for the call) for either weight form."""
+    """(N, K, weight pointer, its row stride, scales pointer, scales row stride, the
+    tensors those pointers are into, kept alive for the call) for either weight form."""
     if isinstance(w, tuple):
         packed, sc = w
         _need_cuda("packed", packed)
-        if packed.dtype not in (torch.int8, torch.uint8) or packed.dim() != 2:
+        p_dtype = packed.dtype
+        if (p_dtype is not torch.int8 and p_dtype is not torch.uint8) or packed.dim() != 2:
             raise TypeError("packed weights must be a 2-D int8 tensor")
-        if sc.dtype != torch.float16 or sc.dim() != 2:
+        if sc.dtype is not torch.float16 or sc.dim() != 2:
             raise TypeError("scales must be a 2-D float16 tensor")
-        N, K = packed.shape[0], packed.shape[1] * 2
-        if sc.shape[0] != N or sc.shape[1] * groupsize != K:
+        N, half_k = packed.shape
+        K = half_k * 2
+        sc_rows, sc_cols = sc.shape
+        if sc_rows != N or sc_cols * groupsize != K:
             raise ValueError(f"scales {tuple(sc.shape)} do not match packed {tuple(packed.shape)}")
-        wt = _rows16(packed, 1)
-        if sc.stride(-1) != 1:
+        wt, w_stride, w_ptr = _rows16(packed, 1)
+        sc_st = sc.stride()
+        if sc_st[1] != 1:
             sc = sc.contiguous()
-        return N, K, wt, wt.stride(0), sc.data_ptr(), sc.stride(0), sc
+            sc_st = sc.stride()
+        return N, K, w_ptr, w_stride, sc.data_ptr(), sc_st[0], (wt, sc)
     _need_cuda("w", w)
-    if w.dtype != torch.float16 or w.dim() != 2:
+    if w.dtype is not torch.float16 or w.dim() != 2:
         raise TypeError("w must be a 2-D float16 tensor or a (packed, scales) tuple")
     N, K = w.shape
-    wt = _rows16(w, 2)
-    return N, K, wt, wt.stride(0), None, 0, None
+    wt, w_stride, w_ptr = _rows16(w, 2)
+    return N, K, w_ptr, w_stride, None, 0, wt
 
 
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5) -> torch.Tensor:
@@ -148,15 +164,15 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5) -> torch.
     hidden = x.shape[-1]
     if weight.shape != (hidden,):
         raise ValueError(f"weight {tuple(weight.shape)} does not match hidden {hidden}")
-    if x.dtype != torch.float16:
+    if x.dtype is not torch.float16:
         x = x.to(torch.float16)
-    wt = weight.to(device=x.device, dtype=torch.float16).contiguous()
-    x2 = _rows16(x.reshape(-1, hidden), 2)
-    out = torch.empty(x2.shape, dtype=torch.float16, device=x.device)
-    if x2.shape[0]:
-        rc = _lib.load().fi_rmsnorm(x2.data_ptr(), x2.stride(0), x2.shape[0], hidden,
-                                    wt.data_ptr(), float(eps), out.data_ptr(), out.stride(0),
-                                    _lib.stream_handle(x.device))
+    wt = _norm_weight(weight, x)
+    x2, x_stride, x_ptr = _rows16(x.reshape(-1, hidden), 2)
+    rows = x2.shape[0]
+    out = torch.empty(rows, hidden, dtype=torch.float16, device=x.device)
+    if rows:
+        rc = _lib.load().fi_rmsnorm(x_ptr, x_stride, rows, hidden, wt.data_ptr(), float(eps),
+                                    out.data_ptr(), hidden, _lib.tensor_stream(x))
         _lib.check(rc, "rms_norm")
     return out.reshape(x.shape)
 
@@ -169,33 +185,32 @@ def rms_norm_int4_matmul(x: torch.Tensor, norm_weight: torch.Tensor, w, eps: flo
     weights with a group size other than 128 take the fp16 form, as in ``int4_matmul``."""
     _need_cuda("x", x)
     w = _other_group_size(w, groupsize)
-    N, K, wt, w_stride, s_ptr, s_stride, _keep = _weight_args(w, groupsize)
-    if x.shape[-1] != K or norm_weight.shape != (K,):
-        raise ValueError(f"x {tuple(x.shape)} / norm weight {tuple(norm_weight.shape)} do not "
+    N, K, w_ptr, w_stride, s_ptr, s_stride, _keep = _weight_args(w, groupsize)
+    x_shape = x.shape
+    if x_shape[-1] != K or norm_weight.shape != (K,):
+        raise ValueError(f"x {tuple(x_shape)} / norm weight {tuple(norm_weight.shape)} do not "
                          f"match K = {K}")
     if K % groupsize:
         raise ValueError(f"K ({K}) must be multiple of groupsize ({groupsize})")
-    if x.dtype != torch.float16:
+    if x.dtype is not torch.float16:
         x = x.to(torch.float16)
-    nw = norm_weight.to(device=x.device, dtype=torch.float16).contiguous()
-    lead = x.shape[:-1]
-    x2 = _rows16(x.reshape(-1, K), 2)
+    nw = _norm_weight(norm_weight, x)
+    x2, x_stride, x_ptr = _rows16(x if len(x_shape) == 2 else x.reshape(-1, K), 2)
     M = x2.shape[0]
     out = torch.empty(M, N, dtype=torch.float16, device=x.device)
     if M == 0 or N == 0:
-        return out.reshape(*lead, N)
-    lib = _lib.load()
-    stream = _lib.stream_handle(x.device)
-    need = lib.fi_rmsnorm_int4_matmul_workspace_size(M, N, K)
+        return out if len(x_shape) == 2 else out.reshape(*x_shape[:-1], N)
+    stream = _lib.tensor_stream(x)
+    need = _lib.workspace_size("fi_rmsnorm_int4_matmul_workspace_size", M, N, K)
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = _workspace(x.device, stream, need)
     ws_ptr = workspace.data_ptr() if need else None
     ws_bytes = workspace.numel() * workspace.element_size() if need else 0
-    rc = lib.fi_rmsnorm_int4_matmul(x2.data_ptr(), x2.stride(0), M, K, nw.data_ptr(), float(eps),
-                                    wt.data_ptr(), w_stride, s_ptr, s_stride, N, groupsize,
-                                    out.data_ptr(), out.stride(0), ws_ptr, ws_bytes, stream)
+    rc = _lib.load().fi_rmsnorm_int4_matmul(x_ptr, x_stride, M, K, nw.data_ptr(), float(eps),
+                                            w_ptr, w_stride, s_ptr, s_stride, N, groupsize,
+                                            out.data_ptr(), N, ws_ptr, ws_bytes, stream)
     _lib.check(rc, "rms_norm_int4_matmul")
-    return out.reshape(*lead, N)
+    return out if len(x_shape) == 2 else out.reshape(*x_shape[:-1], N)
 
 
 def quantize_int4_groupwise(w: torch.Tensor, groupsize: int = 128
@@ -209,11 +224,11 @@ def quantize_int4_groupwise(w: torch.Tensor, groupsize: int = 128
     N, K = w.shape
     if K % groupsize:
         raise ValueError(f"K ({K}) must be multiple of groupsize ({groupsize})")
-    wt = _rows16(w, 2)
+    wt, w_stride, w_ptr = _rows16(w, 2)
     packed = torch.empty(N, K // 2, dtype=torch.int8, device=w.device)
     scales = torch.empty(N, K // groupsize, dtype=torch.float16, device=w.device)
     lib = _lib.load()
-    rc = lib.fi_int4_quantize(wt.data_ptr(), wt.stride(0), N, K, groupsize, packed.data_ptr(),
+    rc = lib.fi_int4_quantize(w_ptr, w_stride, N, K, groupsize, packed.data_ptr(),
                               packed.stride(0), scales.data_ptr(), scales.stride(0),
                               _lib.stream_handle(w.device))
     _lib.check(rc, "quantize_int4_groupwise")

@@ -29,31 +29,43 @@ def precompute_freqs(head_dim: int, max_seq_len: int, theta: float = 500000.0,
     return angles.cos(), angles.sin()
 
 
+# rope_store_kv runs once per layer and decode step, where its host time is of the order of
+# the kernel's: tensors' shapes, strides and pointers are read once each, dtypes compared by
+# identity and devices by index.
+
 def _check_rows(name: str, t: torch.Tensor, heads: int | None = None,
-                head_dim: int | None = None) -> None:
-    if t.dtype != torch.float16:
+                head_dim: int | None = None) -> torch.Size:
+    """Validates a [batch, tokens, heads, head_dim] fp16 HIP tensor; returns its shape."""
+    if t.dtype is not torch.float16:
         raise TypeError(f"{name} must be float16, got {t.dtype}")
-    if t.device.type != "cuda":
+    if not t.is_cuda:
         raise RuntimeError(f"{name} must be on a HIP device; fast_infer_amd has no CPU path")
-    if t.dim() != 4 or t.shape[-1] % 16 or (head_dim is not None and t.shape[-1] != head_dim):
+    shape = t.shape
+    if len(shape) != 4 or shape[3] % 16 or (head_dim is not None and shape[3] != head_dim):
         raise ValueError(f"{name} must be [batch, tokens, heads, head_dim] with head_dim a "
                          f"multiple of 16{'' if head_dim is None else f' ({head_dim})'}, "
-                         f"got {tuple(t.shape)}")
-    if heads is not None and t.shape[2] != heads:
-        raise ValueError(f"{name} has {t.shape[2]} heads, expected {heads}")
+                         f"got {tuple(shape)}")
+    if heads is not None and shape[2] != heads:
+        raise ValueError(f"{name} has {shape[2]} heads, expected {heads}")
+    return shape
 
 
-def _rows(t: torch.Tensor) -> torch.Tensor:
-    if t.stride(-1) != 1 or any(s % 8 for s in t.stride()[:-1]) or t.data_ptr() % 16:
-        return t.contiguous()
-    return t
+def _rows(t: torch.Tensor) -> tuple[torch.Tensor, tuple, int]:
+    """(t or a contiguous copy, its strides, its pointer): unit inner stride, other strides
+    multiples of 8 elements, 16-byte aligned base."""
+    st, ptr = t.stride(), t.data_ptr()
+    if st[3] != 1 or st[0] % 8 or st[1] % 8 or st[2] % 8 or ptr % 16:
+        t = t.contiguous()
+        st, ptr = t.stride(), t.data_ptr()
+    return t, st, ptr
 
 
-def _table(name: str, t: torch.Tensor, device, head_dim: int) -> torch.Tensor:
+def _table(name: str, t: torch.Tensor, dev: int, head_dim: int) -> torch.Tensor:
+    """A cos or sin table as fp16 [rows, head_dim] on device index `dev`, contiguous."""
     if t.dim() != 2 or t.shape[1] != head_dim:
         raise ValueError(f"{name} must be [rows, {head_dim}], got {tuple(t.shape)}")
-    if t.dtype != torch.float16 or t.device != device:
-        t = t.to(device=device, dtype=torch.float16)
+    if t.dtype is not torch.float16 or t.get_device() != dev:
+        t = t.to(device=torch.device("cuda", dev), dtype=torch.float16)
     return t if t.is_contiguous() and t.data_ptr() % 16 == 0 else t.contiguous()
 
 
@@ -73,70 +85,82 @@ def rope_store_kv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor | None,
     a scalar ``start_pos`` (the reference's table indexing fails there); with
     ``start_positions`` such tokens are skipped on the device, their q/k rows left
     unwritten.  Returns (q_rot, k_rot or None)."""
-    _check_rows("q", q)
-    batch, tokens, num_q_heads, head_dim = q.shape
-    _check_rows("k", k, head_dim=head_dim)
-    num_kv_heads = k.shape[2]
-    if k.shape[:2] != q.shape[:2]:
-        raise ValueError(f"k {tuple(k.shape)} does not match q {tuple(q.shape)}")
+    q_shape = _check_rows("q", q)
+    batch, tokens, num_q_heads, head_dim = q_shape
+    k_shape = _check_rows("k", k, head_dim=head_dim)
+    num_kv_heads = k_shape[2]
+    if k_shape[0] != batch or k_shape[1] != tokens:
+        raise ValueError(f"k {tuple(k_shape)} does not match q {tuple(q_shape)}")
+    dev = q.get_device()
     pool = k_cache is not None
     if pool:
         if v is None or v_cache is None or block_table is None:
             raise ValueError("the pool write needs v, v_cache and block_table")
-        _check_rows("v", v, num_kv_heads, head_dim)
-        if v.shape[:2] != q.shape[:2]:
-            raise ValueError(f"v {tuple(v.shape)} does not match q {tuple(q.shape)}")
+        v_shape = _check_rows("v", v, num_kv_heads, head_dim)
+        if v_shape[0] != batch or v_shape[1] != tokens:
+            raise ValueError(f"v {tuple(v_shape)} does not match q {tuple(q_shape)}")
         for name, t in (("k_cache", k_cache), ("v_cache", v_cache)):
-            if t.dtype != torch.float16 or t.device.type != "cuda":
+            if t.dtype is not torch.float16 or not t.is_cuda:
                 raise TypeError(f"{name} must be a float16 HIP tensor")
-        if (k_cache.dim() != 4 or v_cache.shape != k_cache.shape
-                or k_cache.shape[2] != num_kv_heads or k_cache.shape[3] != head_dim):
-            raise ValueError(f"pool {tuple(k_cache.shape)} does not match k {tuple(k.shape)}")
+        pool_shape = k_cache.shape
+        if (len(pool_shape) != 4 or v_cache.shape != pool_shape
+                or pool_shape[2] != num_kv_heads or pool_shape[3] != head_dim):
+            raise ValueError(f"pool {tuple(pool_shape)} does not match k {tuple(k_shape)}")
         if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
             raise ValueError("pools must be contiguous")
-        if block_table.dtype != torch.int32 or block_table.dim() != 2:
+        if block_table.dtype is not torch.int32 or block_table.dim() != 2:
             raise TypeError("block_table must be a 2-D int32 tensor")
-        if block_table.shape[0] < batch:
+        bt_rows, bt_cols = block_table.shape
+        if bt_rows < batch:
             raise ValueError("block_table has fewer rows than the batch")
         if block_table.stride(-1) != 1:
             block_table = block_table.contiguous()
-    cos_t = _table("cos_table", cos_table, q.device, head_dim)
-    sin_t = _table("sin_table", sin_table, q.device, head_dim)
-    if cos_t.shape != sin_t.shape:
+    cos_t = _table("cos_table", cos_table, dev, head_dim)
+    sin_t = _table("sin_table", sin_table, dev, head_dim)
+    table_rows = cos_t.shape[0]
+    if sin_t.shape[0] != table_rows:
         raise ValueError("cos and sin tables differ in shape")
     if start_positions is not None:
-        start_positions = start_positions.to(device=q.device, dtype=torch.int32).contiguous()
+        if (start_positions.dtype is not torch.int32 or start_positions.get_device() != dev
+                or not start_positions.is_contiguous()):
+            start_positions = start_positions.to(device=q.device, dtype=torch.int32).contiguous()
         if start_positions.numel() < batch:
             raise ValueError("start_positions has fewer entries than the batch")
-    elif tokens > 0 and (start_pos < 0 or start_pos + tokens > cos_t.shape[0]):
+    elif tokens > 0 and (start_pos < 0 or start_pos + tokens > table_rows):
         raise IndexError(f"positions {start_pos}..{start_pos + tokens - 1} outside the "
-                         f"{cos_t.shape[0]}-row table")
+                         f"{table_rows}-row table")
     if q_out is None:
-        q_out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
-    elif q_out.shape != q.shape:
+        q_out = torch.empty(q_shape, dtype=q.dtype, device=q.device)
+    elif q_out.shape != q_shape:
         raise ValueError("q_out must have q's shape")
-    k_out = torch.empty(k.shape, dtype=k.dtype, device=k.device) if return_k else None
+    k_out = torch.empty(k_shape, dtype=k.dtype, device=k.device) if return_k else None
     if batch == 0 or tokens == 0:
         return q_out, k_out
-    q, k = _rows(q), _rows(k)
-    v = _rows(v) if v is not None else None
-    lib = _lib.load()
-    rc = lib.fi_rope_store_kv(
-        q.data_ptr(), q.stride(0), q.stride(1), q.stride(2),
-        k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
-        v.data_ptr() if v is not None else None,
-        *(v.stride()[:3] if v is not None else (0, 0, 0)),
-        cos_t.data_ptr(), sin_t.data_ptr(), cos_t.shape[0],
-        q_out.data_ptr(), q_out.stride(0), q_out.stride(1), q_out.stride(2),
-        k_out.data_ptr() if k_out is not None else None,
-        *(k_out.stride()[:3] if k_out is not None else (0, 0, 0)),
-        k_cache.data_ptr() if pool else None, v_cache.data_ptr() if pool else None,
-        k_cache.shape[0] if pool else 0, k_cache.shape[1] if pool else 0,
-        block_table.data_ptr() if pool else None,
-        block_table.stride(0) if pool else 0, block_table.shape[1] if pool else 0,
+    q, qs, q_ptr = _rows(q)
+    k, ks, k_ptr = _rows(k)
+    if v is not None:
+        v, vs, v_ptr = _rows(v)
+    else:
+        vs, v_ptr = (0, 0, 0), None
+    qo = q_out.stride()
+    if k_out is not None:
+        ko, ko_ptr = k_out.stride(), k_out.data_ptr()
+    else:
+        ko, ko_ptr = (0, 0, 0), None
+    if pool:
+        kc_ptr, vc_ptr, n_blocks, bs = k_cache.data_ptr(), v_cache.data_ptr(), pool_shape[0], pool_shape[1]
+        bt_ptr, bt_stride = block_table.data_ptr(), block_table.stride(0)
+    else:
+        kc_ptr = vc_ptr = bt_ptr = None
+        n_blocks = bs = bt_stride = bt_cols = 0
+    rc = _lib.load().fi_rope_store_kv(
+        q_ptr, qs[0], qs[1], qs[2], k_ptr, ks[0], ks[1], ks[2], v_ptr, vs[0], vs[1], vs[2],
+        cos_t.data_ptr(), sin_t.data_ptr(), table_rows,
+        q_out.data_ptr(), qo[0], qo[1], qo[2], ko_ptr, ko[0], ko[1], ko[2],
+        kc_ptr, vc_ptr, n_blocks, bs, bt_ptr, bt_stride, bt_cols,
         batch, tokens, num_q_heads, num_kv_heads, head_dim,
         int(start_pos), None if start_positions is None else start_positions.data_ptr(),
-        _lib.stream_handle(q.device))
+        _lib.tensor_stream(q))
     _lib.check(rc, "rope_store_kv")
     return q_out, k_out
 
