@@ -15,7 +15,7 @@
 //                    the stream has no counters);
 //   17..128          gemm_kernel (packed weights from 65 rows), below;
 //   >= 129           the weight dequantized once into the workspace, then
-//                    ping_pong_gemm_kernel, an fp16 GEMM.
+//                    wide_gemm_kernel, an fp16 GEMM.
 //
 // gemm_kernel: one workgroup = 4 waves = 64 output columns (16 per wave) x MT rows, over a
 // slice of the K groups.  Per 128-wide group, X[MT, 128] is staged in LDS (double
@@ -690,31 +690,31 @@ __device__ __attribute__((aligned(256))) unsigned sk_counters[kSkStreamSlots * k
 
 // Prefill-sized calls: the MFMA kernels above spend most of their time dequantizing (each
 // weight is dequantized once per row tile) at these sizes, so the weight is dequantized once
-// into the workspace and a plain fp16 GEMM runs on it: ping_pong_gemm_kernel.
+// into the workspace and a plain fp16 GEMM runs on it: wide_gemm_kernel.
 //
 // C[M, N] = X[M, K] * W[N, K]^T, fp16 in and out, fp32 accumulation, K a multiple of 64.
-// One workgroup per 256 x 256 tile of C, eight waves, two per SIMD: waves w and w + 4 share
-// SIMD w % 4 (checked on gfx950 with a probe reading HW_REG_HW_ID).  Wave w owns 64 rows
-// (m, 64 * (w / 2)..) x 128 columns (n, 128 * (w % 2)..) of the tile: 8 x 4 MFMA tiles of
-// v_mfma_f32_16x16x32_f16, W as the A operand and X^T as the B operand, 128 fp32 sums.
-// Per 64-wide K step the tile's X and W rows (128 bytes each, 16-byte chunk c of row r at
-// slot c ^ ((r / 2) % 8), so the 16 rows a quarter-wave reads fall on distinct banks) are
-// copied global->LDS with buffer_load ... lds into one of two 64 KiB stages.
-// The two halves of the workgroup (waves 0-3, waves 4-7) take turns, one barrier-separated
-// phase apart: while one half runs its step's 64 MFMAs on fragments held in registers, the
-// other reads the next step's 24 fragments from LDS and issues copies.  Each SIMD then
-// always has one wave feeding its matrix core and one loading, without either waiting for
-// the other's LDS latency.  Copies of step t + 1 go out two phases after the last read of
-// their stage and are waited for (vmcnt) by the wave that issued them before the phase in
-// which step t + 1 is first read.
-constexpr int kPpTile = 256;             // rows and columns of C per workgroup
-constexpr int kPpK = 64;                 // K per step
-constexpr int kPpThreads = 512;
-constexpr int kPpRowB = kPpK * 2;        // bytes per LDS row
-constexpr int kPpOperand = kPpTile * kPpRowB;  // 32 KiB: X or W rows of one step
-constexpr int kPpStage = 2 * kPpOperand;       // 64 KiB: X rows, then W rows
+// One workgroup per 256 x 256 tile of C, four waves, one per SIMD.  Wave w owns 128 rows
+// (m, 128 * (w / 2)..) x 128 columns (n, 128 * (w % 2)..) of the tile: 8 x 8 MFMA tiles of
+// v_mfma_f32_16x16x32_f16, W as the A operand and X^T as the B operand, 256 fp32 sums held
+// in the accumulation registers (AGPRs), so each 16-byte fragment read from LDS feeds eight
+// MFMAs (a 64 x 128 wave tile feeds four to eight).  Per 64-wide K step the tile's X and W
+// rows (128 bytes each, 16-byte chunk c of row r at slot c ^ ((r / 2) % 8), so the 16 rows a
+// quarter-wave reads fall on distinct banks) are copied global->LDS with buffer_load ... lds
+// into one of two 64 KiB stages.  A step is two k-substeps of 64 MFMAs: the second
+// substep's 16 fragments are read between the first substep's MFMAs; after 48 of the second
+// substep's MFMAs the wave waits for its copies of the next step and passes a barrier (every
+// wave has then read this step's stage and landed the next), and the next step's first
+// fragments are read between the last 16 MFMAs.  The copies of step t + 1 go out between
+// the first substep's MFMAs of step t, into the stage every wave finished reading before
+// the previous step's barrier.
+constexpr int kGemmTile = 256;                     // rows and columns of C per workgroup
+constexpr int kGemmK = 64;                         // K per step
+constexpr int kGemmThreads = 256;
+constexpr int kGemmRowB = kGemmK * 2;              // bytes per LDS row
+constexpr int kGemmOperand = kGemmTile * kGemmRowB;  // 32 KiB: X or W rows of one step
+constexpr int kGemmStage = 2 * kGemmOperand;         // 64 KiB: X rows, then W rows
 
-struct PpParams {
+struct GemmParams {
   const half_t* x;
   int64_t ldx;
   const half_t* w;
@@ -727,23 +727,11 @@ struct PpParams {
   int vec_out;  // output rows 16-byte aligned and N % 8 == 0: 16-byte stores
 };
 
-// A workgroup barrier that nothing crosses: the compiler's scheduler may not move
-// instructions (MFMAs included) over it, nor memory accesses (the copies are inline asm it
-// does not track).
-__device__ __forceinline__ void pp_barrier() {
-  __builtin_amdgcn_sched_barrier(0);
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_sched_barrier(0);
-}
-
-__global__ __launch_bounds__(kPpThreads, 1) void ping_pong_gemm_kernel(PpParams p) {
-  __shared__ __attribute__((aligned(16))) char lds[2 * kPpStage];
+__global__ __launch_bounds__(kGemmThreads, 1) void wide_gemm_kernel(GemmParams p) {
+  __shared__ __attribute__((aligned(16))) char lds[2 * kGemmStage];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int half = wave >> 2;               // 0: waves 0-3, 1: waves 4-7 (one phase behind)
-  const int wn = wave & 1, wm = wave >> 1;  // wave tile: columns 128 * wn.., rows 64 * wm..
+  const int wn = wave & 1, wm = wave >> 1;  // wave tile: columns 128 * wn.., rows 128 * wm..
   // Tile order: with p.band, block id L runs on XCD L % 8 and XCD e takes row tiles
   // e * band .. e * band + band - 1 against every column tile, so the X rows of its tiles
   // stay in its own L2; otherwise row tiles vary fastest.
@@ -759,98 +747,120 @@ __global__ __launch_bounds__(kPpThreads, 1) void ping_pong_gemm_kernel(PpParams 
       tn = L / p.tiles_m;
     }
   }
-  const int m0 = tm * kPpTile, n0 = tn * kPpTile;
-  const int rows_x = min(kPpTile, p.M - m0), rows_w = min(kPpTile, p.N - n0);
+  const int m0 = tm * kGemmTile, n0 = tn * kGemmTile;
+  const int rows_x = min(kGemmTile, p.M - m0), rows_w = min(kGemmTile, p.N - n0);
   // descriptors over exactly the tile's rows: lanes of rows past M or N read zeros
   const rsrc_t xr = raw_rsrc(p.x + (int64_t)m0 * p.ldx,
                              (int)(((int64_t)(rows_x - 1) * p.ldx + p.K) * 2));
   const rsrc_t wr = raw_rsrc(p.w + (int64_t)n0 * p.ldw,
                              (int)(((int64_t)(rows_w - 1) * p.ldw + p.K) * 2));
-  // this wave copies rows 32w .. 32w + 31 of X and of W: four instructions of 8 rows each
+  // this wave copies rows 64w .. 64w + 63 of X and of W: eight instructions of 8 rows each
   // per operand; lane l fills slot l % 8 of row r0 + l / 8 with chunk (l % 8) ^ ((r / 2) % 8)
-  int xoff[4], woff[4];
+  int xoff[8], woff[8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = 32 * wave + 8 * i + (lane >> 3);
+  for (int i = 0; i < 8; ++i) {
+    const int r = 64 * wave + 8 * i + (lane >> 3);
     const int c = (lane & 7) ^ ((r >> 1) & 7);
     xoff[i] = r < rows_x ? (int)((int64_t)r * p.ldx * 2) + (c << 4) : 0x7ffffff0;
     woff[i] = r < rows_w ? (int)((int64_t)r * p.ldw * 2) + (c << 4) : 0x7ffffff0;
   }
   const uint32_t lds0 = lds_addr(lds);
-  const int steps = p.K / kPpK;
-  auto issue = [&](int kt) {
-    const uint32_t base = lds0 + (kt & 1) * kPpStage;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      lds_copy16(xr, base + (32 * wave + 8 * i) * kPpRowB, xoff[i], kt * kPpRowB);
-      lds_copy16(wr, base + kPpOperand + (32 * wave + 8 * i) * kPpRowB, woff[i], kt * kPpRowB);
-    }
+  const int steps = p.K / kGemmK;
+  // copy q (0..15) of step kt: X rows for q < 8, W rows for q >= 8
+  auto copy = [&](int kt, int q) {
+    const uint32_t base = lds0 + (kt & 1) * kGemmStage;
+    if (q < 8)
+      lds_copy16(xr, base + (64 * wave + 8 * q) * kGemmRowB, xoff[q], kt * kGemmRowB);
+    else
+      lds_copy16(wr, base + kGemmOperand + (64 * wave + 8 * (q - 8)) * kGemmRowB, woff[q - 8],
+                 kt * kGemmRowB);
   };
 
-  floatx4 acc[8][4];
+  floatx4 acc[8][8];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 8; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  // fragment (k-substep s, tile i): row 16i + fr, chunk 4s + fg; rows 16i + fr share
-  // (row / 2) % 8 with row fr
+  // fragment q of k-substep s: W tile q (q < 8) or X tile q - 8, row 16 * tile + fr, chunk
+  // 4s + fg; rows 16i + fr share (row / 2) % 8 with row fr
   const int fr = lane & 15, fg = lane >> 4;
   const int sw = (fr >> 1) & 7;
-  const int xrow0 = (64 * wm + fr) * kPpRowB, wrow0 = kPpOperand + (128 * wn + fr) * kPpRowB;
-  half8 wf[2][8], xf[2][4];
+  const int xrow0 = (128 * wm + fr) * kGemmRowB;
+  const int wrow0 = kGemmOperand + (128 * wn + fr) * kGemmRowB;
+  auto frag = [&](const char* st, int s, int q) {
+    const int row0 = q < 8 ? wrow0 + q * 16 * kGemmRowB : xrow0 + (q - 8) * 16 * kGemmRowB;
+    return as_half8(*(const u32x4*)(st + row0 + (((4 * s + fg) ^ sw) << 4)));
+  };
+  half8 f0[16], f1[16];
+  // the scheduler keeps each group of MFMAs with its reads and copies (sched_barrier)
+  auto fence = [] { __builtin_amdgcn_sched_barrier(0); };
 
-  issue(0);
-  if (steps > 1) issue(1);
-  if (steps > 1)
-    wait_vmcnt<8>();  // step 0 (loads complete in issue order)
-  else
-    wait_vmcnt<0>();
-  pp_barrier();
-  if (half) pp_barrier();  // waves 4-7 start one phase later
-  for (int kt = 0; kt < steps; ++kt) {
-    // LOAD phase: this step's fragments.  Waves 0-3 also copy step kt + 1 into the stage
-    // of step kt - 1, which waves 4-7 finished reading in the previous phase.
-    {
-      const char* st = lds + (kt & 1) * kPpStage;
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
+  for (int q = 0; q < 16; ++q) copy(0, q);
+  wait_vmcnt<0>();
+  __builtin_amdgcn_s_barrier();
+  fence();
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-          wf[s][i] = as_half8(
-              *(const u32x4*)(st + wrow0 + i * 16 * kPpRowB + (((4 * s + fg) ^ sw) << 4)));
+  for (int q = 0; q < 16; ++q) f0[q] = frag(lds, 0, q);
+  fence();
+  auto step = [&](int kt, auto more_c) {
+    constexpr bool more = decltype(more_c)::value;  // a step follows
+    const char* st = lds + (kt & 1) * kGemmStage;
+    // substep 0 on f0; substep 1's fragments read and the next step's copies issued
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          xf[s][j] = as_half8(
-              *(const u32x4*)(st + xrow0 + j * 16 * kPpRowB + (((4 * s + fg) ^ sw) << 4)));
+    for (int g = 0; g < 16; ++g) {
+      f1[g] = frag(st, 1, g);
+      if constexpr (more) copy(kt + 1, g);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int e = 4 * g + t, i = e >> 3, j = e & 7;
+        acc[i][j] = mfma16x16x32(f0[i], f0[8 + j], acc[i][j]);
       }
-      if (half == 0 && kt >= 1 && kt + 1 < steps) issue(kt + 1);
-      wait_lgkmcnt0();  // the stage may be refilled once this phase ends
-      if (half == 1) wait_vmcnt<0>();  // this wave's copies of step kt + 1
+      fence();
     }
-    pp_barrier();
-    // COMPUTE phase: 64 MFMAs on registers.  Waves 4-7 copy step kt + 2 into the stage of
-    // step kt, which both halves have now read.
-    {
-      if (half == 1 && kt + 2 < steps) issue(kt + 2);
+    // substep 1 on f1: 48 MFMAs, the wait and barrier, then 16 MFMAs with the next step's
+    // substep-0 fragments read between them
 #pragma unroll
-      for (int s = 0; s < 2; ++s)
+    for (int g = 0; g < 12; ++g) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) acc[i][j] = mfma16x16x32(wf[s][i], xf[s][j], acc[i][j]);
-      if (half == 0) wait_vmcnt<0>();  // this wave's copies of step kt + 1
+      for (int t = 0; t < 4; ++t) {
+        const int e = 4 * g + t, i = e >> 3, j = e & 7;
+        acc[i][j] = mfma16x16x32(f1[i], f1[8 + j], acc[i][j]);
+      }
+      fence();
     }
-    pp_barrier();
-  }
-  if (!half) pp_barrier();  // every wave passes the same number of barriers
+    if constexpr (more) {
+      wait_vmcnt<0>();
+      __builtin_amdgcn_s_barrier();
+      fence();
+    }
+    const char* nst = lds + ((kt + 1) & 1) * kGemmStage;
+#pragma unroll
+    for (int g = 12; g < 16; ++g) {
+      if constexpr (more) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) f0[4 * (g - 12) + u] = frag(nst, 0, 4 * (g - 12) + u);
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int e = 4 * g + t, i = e >> 3, j = e & 7;
+        acc[i][j] = mfma16x16x32(f1[i], f1[8 + j], acc[i][j]);
+      }
+      fence();
+    }
+  };
+  for (int kt = 0; kt + 1 < steps; ++kt) step(kt, std::true_type{});
+  step(steps - 1, std::false_type{});
+  __builtin_amdgcn_s_barrier();  // every wave is done with the stages
+  fence();
 
   // Lane (m = 16j + fr, fg) holds C[m][16i + 4fg .. +3] of the wave's block.  Rows go
-  // through the wave's own 16 KiB of LDS (fp16, 256 bytes a row, chunk c of row m at
+  // through the wave's own 32 KiB of LDS (fp16, 256 bytes a row, chunk c of row m at
   // c ^ (m % 16)) so that 16 lanes store one row's 256 bytes.
-  char* cs = lds + wave * (64 * 256);
+  char* cs = lds + wave * (128 * 256);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < 8; ++j) {
     const int m = 16 * j + fr;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -862,10 +872,10 @@ __global__ __launch_bounds__(kPpThreads, 1) void ping_pong_gemm_kernel(PpParams 
   const int sr = lane >> 4, sc = lane & 15;
   const int gn = n0 + 128 * wn + 8 * sc;
 #pragma unroll 4
-  for (int q = 0; q < 16; ++q) {
+  for (int q = 0; q < 32; ++q) {
     const int m = 4 * q + sr;
     const u32x4 v = *(const u32x4*)(cs + m * 256 + ((sc ^ (m & 15)) << 4));
-    const int gm = m0 + 64 * wm + m;
+    const int gm = m0 + 128 * wm + m;
     if (gm >= p.M || gn >= p.N) continue;
     half_t* dst = p.o + (int64_t)gm * p.ldo + gn;
     if (p.vec_out) {
@@ -883,11 +893,11 @@ __global__ __launch_bounds__(kPpThreads, 1) void ping_pong_gemm_kernel(PpParams 
 // K a multiple of 64, rows of X and W 16-byte aligned.
 inline int f16_gemm(const half_t* x, int64_t ldx, const half_t* w, int64_t ldw, half_t* out,
                     int64_t ldc, int64_t M, int64_t N, int64_t K, hipStream_t st) {
-  if (K % kPpK || ((int64_t)(kPpTile - 1) * std::max(ldx, ldw) + K) * 2 >= 0x7ffffff0) {
+  if (K % kGemmK || ((int64_t)(kGemmTile - 1) * std::max(ldx, ldw) + K) * 2 >= 0x7ffffff0) {
     set_error("fi_int4_matmul: 256 rows of X or W span 2^31 bytes or more");
     return FI_ERR_UNSUPPORTED;
   }
-  PpParams p;
+  GemmParams p;
   p.x = x;
   p.ldx = ldx;
   p.w = w;
@@ -897,8 +907,8 @@ inline int f16_gemm(const half_t* x, int64_t ldx, const half_t* w, int64_t ldw, 
   p.M = (int)M;
   p.N = (int)N;
   p.K = (int)K;
-  p.tiles_m = (int)((M + kPpTile - 1) / kPpTile);
-  const int64_t tiles_n = (N + kPpTile - 1) / kPpTile;
+  p.tiles_m = (int)((M + kGemmTile - 1) / kGemmTile);
+  const int64_t tiles_n = (N + kGemmTile - 1) / kGemmTile;
   const int64_t tiles = p.tiles_m * tiles_n;
   if (tiles > 0x7fffffff) {
     set_error("fi_int4_matmul: too many output tiles");
@@ -906,7 +916,7 @@ inline int f16_gemm(const half_t* x, int64_t ldx, const half_t* w, int64_t ldw, 
   }
   p.band = p.tiles_m % 8 == 0 ? p.tiles_m / 8 : 0;
   p.vec_out = ((uintptr_t)out & 15) == 0 && ldc % 8 == 0 && N % 8 == 0;
-  hipLaunchKernelGGL(ping_pong_gemm_kernel, dim3((unsigned)tiles), dim3(kPpThreads), 0, st, p);
+  hipLaunchKernelGGL(wide_gemm_kernel, dim3((unsigned)tiles), dim3(kGemmThreads), 0, st, p);
   return check_launch("fi_int4_matmul");
 }
 

@@ -189,7 +189,7 @@ def test_int4_matmul_prefill_size_sampled(hip):
 
 
 # 129 rows and up: the weight dequantized once, then the 256 x 256-tile fp16 GEMM
-# (ping_pong_gemm_kernel).  Shapes: partial row and column tiles, two K steps (K 128) and
+# (wide_gemm_kernel).  Shapes: partial row and column tiles, two K steps (K 128) and
 # 128 (K 8192), row tiles in multiples of 8 (the XCD-banded tile order, also with a partial
 # last row tile) and not, N not a multiple of 8 (element stores), output rows with a stride
 # and an output that is only 2-byte aligned (element stores), X rows with a stride; packed
